@@ -1,0 +1,137 @@
+/*
+ * mpattn.h -- C ABI of the MI355X (gfx950) multi-pathway attention library
+ * (libmpattn.so).
+ *
+ * The op: for batch b, head h, query i and key j
+ *
+ *   s_ij = scale * <R_i q_self_i, R_j k_self_j>   if chain[b,i] == chain[b,j]
+ *        = scale * <q_multi_i, k_multi_j>         otherwise
+ *   s_ij = -inf                                   if key j is padded
+ *   P_i  = softmax_j(s_i)          (one softmax over both pathways)
+ *   O_i  = sum_j P_ij * (v_self_j if same chain else v_multi_j)
+ *
+ * R_p is the rotary embedding at global position p (half-split layout,
+ * inv_freq = 10000^(-2i/D)); it is applied only when rope == MPATTN_ROPE_FUSED.
+ * A query row whose keys are all padded produces O_i = 0.
+ *
+ * Reference interfaces (molecular-william/mint_plus, which binds no FFI; these
+ * entry points replace the Python/Triton functions named on each one):
+ *   mpattn_fwd  -> mint_plus/models/kernels/multi_pathway_attention.py:184
+ *                  (fused_multi_pathway_attention), its fp16 twin
+ *                  multi_pathway_attention_fp16.py:148, and the eager combine
+ *                  mint_plus/models/modules_plus.py:155-201
+ *   mpattn_bwd  -> mint_plus/models/kernels/multi_pathway_attention_bwd.py:15
+ *                  (fused_multi_pathway_attention_bwd)
+ *   mpattn_combine_fwd / mpattn_combine_bwd
+ *               -> mint_plus/models/kernels/__init__.py:179 and :247
+ *                  (fused_multimer_combine / fused_multimer_combine_bwd)
+ *
+ * Conventions
+ *   - The caller owns and allocates every device buffer (outputs and the
+ *     backward workspace). The library never allocates, never synchronises,
+ *     and keeps no mutable global state: calls on different streams are
+ *     independent.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
+ *   - All tensors are 4-D (B, H, L, D) views given by a base pointer and
+ *     element strides for b, h and t; the head-dim stride must be 1.
+ *     This admits the (L, B, 3E) projection output without a copy.
+ *   - Return 0 on success, a negative MPATTN_ERR_* code on error. Arguments
+ *     are validated before anything is enqueued.
+ */
+#ifndef MPATTN_H
+#define MPATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MPATTN_VERSION 1
+
+enum {
+    MPATTN_OK = 0,
+    MPATTN_ERR_INVALID = -1,      /* bad pointer, shape, stride or enum   */
+    MPATTN_ERR_UNSUPPORTED = -2,  /* valid request this build cannot do   */
+    MPATTN_ERR_LAUNCH = -3,       /* the HIP runtime rejected the launch  */
+};
+
+enum { MPATTN_BF16 = 0, MPATTN_FP16 = 1, MPATTN_FP32 = 2 };
+
+enum {
+    MPATTN_ROPE_NONE = 0,   /* q/k used as given (caller rotated/scaled)   */
+    MPATTN_ROPE_FUSED = 1,  /* rotate q_self/k_self by global position     */
+};
+
+/* 4-D (B, H, L, D) view; strides in elements, head-dim stride is 1. */
+typedef struct mpattn_tensor {
+    const void *ptr;
+    int64_t stride_b, stride_h, stride_t;
+} mpattn_tensor;
+
+typedef struct mpattn_fwd_params {
+    mpattn_tensor q_self, k_self, v_self;   /* self pathway                 */
+    mpattn_tensor q_multi, k_multi, v_multi;/* multimer (cross) pathway     */
+    mpattn_tensor out;                      /* written; same dtype          */
+    float *lse;              /* optional (B,H,L) fp32 log-sum-exp, or NULL  */
+    /* Pathway selection: exactly one of chain_id / chain_mask is non-NULL.
+     * chain_id  : (B, L) int32, contiguous.
+     * chain_mask: (B, L, L) uint8/bool, element strides below; nonzero means
+     *             "different chains" (the reference's self_attn_mask).     */
+    const int32_t *chain_id;
+    const uint8_t *chain_mask;
+    int64_t mask_stride_b, mask_stride_q, mask_stride_k;
+    const uint8_t *key_pad;  /* optional (B, L) contiguous, nonzero = pad   */
+    /* RoPE tables (L, D/2) fp32 contiguous: cos/sin of p * inv_freq[i].
+     * Required when rope == MPATTN_ROPE_FUSED, ignored otherwise.          */
+    const float *rope_cos, *rope_sin;
+    int32_t B, H, L, D;
+    int32_t dtype;           /* MPATTN_BF16 / MPATTN_FP16 / MPATTN_FP32      */
+    int32_t rope;            /* MPATTN_ROPE_NONE / MPATTN_ROPE_FUSED         */
+    float scale;             /* logit scale (> 0), e.g. D^-1/2               */
+    int32_t sqrt_softmax;    /* 1: O = sum sqrt(P) V (muS variant)           */
+    float dropout_p;         /* must be 0                                    */
+} mpattn_fwd_params;
+
+typedef struct mpattn_bwd_params {
+    mpattn_tensor q_self, k_self, v_self, q_multi, k_multi, v_multi;
+    mpattn_tensor out;        /* forward output O                           */
+    mpattn_tensor grad_out;   /* dO                                         */
+    const float *lse;         /* (B,H,L) fp32 from mpattn_fwd               */
+    mpattn_tensor dq_self, dk_self, dv_self, dq_multi, dk_multi, dv_multi;
+    const int32_t *chain_id;
+    const uint8_t *chain_mask;
+    int64_t mask_stride_b, mask_stride_q, mask_stride_k;
+    const uint8_t *key_pad;
+    const float *rope_cos, *rope_sin;
+    void *workspace;          /* >= mpattn_bwd_workspace_size() bytes       */
+    int32_t B, H, L, D;
+    int32_t dtype, rope;
+    float scale;
+    int32_t sqrt_softmax;
+} mpattn_bwd_params;
+
+/* Forward. Replaces fused_multi_pathway_attention
+ * (mint_plus/models/kernels/multi_pathway_attention.py:184-279) and
+ * fused_multi_pathway_attention_fp16 (multi_pathway_attention_fp16.py:148). */
+int mpattn_fwd(const mpattn_fwd_params *p, void *stream);
+
+/* Workspace bytes mpattn_bwd needs for (B, H, L). */
+int64_t mpattn_bwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D);
+
+/* Backward: all six gradients, deterministic (no atomics). Replaces
+ * fused_multi_pathway_attention_bwd
+ * (mint_plus/models/kernels/multi_pathway_attention_bwd.py:15-59). */
+int mpattn_bwd(const mpattn_bwd_params *p, void *stream);
+
+/* Human-readable message for an MPATTN_ERR_* code, and the detail of the
+ * most recent validation failure on the calling thread. */
+const char *mpattn_strerror(int code);
+const char *mpattn_last_error(void);
+int mpattn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MPATTN_H */

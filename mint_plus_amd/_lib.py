@@ -1,0 +1,316 @@
+"""ctypes binding of libmpattn.so (C ABI declared in include/mpattn.h).
+
+Torch is used only for device memory and the current HIP stream: every
+computation of the op happens in the gfx950 kernels behind this ABI. When the
+library is missing, every entry point raises -- there is no CPU fallback.
+"""
+import ctypes
+import os
+import threading
+
+import numpy as np
+import torch
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG_DIR, "libmpattn.so")
+
+MPATTN_OK = 0
+MPATTN_ERR_INVALID = -1
+MPATTN_ERR_UNSUPPORTED = -2
+MPATTN_ERR_LAUNCH = -3
+
+MPATTN_BF16, MPATTN_FP16, MPATTN_FP32 = 0, 1, 2
+MPATTN_ROPE_NONE, MPATTN_ROPE_FUSED = 0, 1
+
+ROPE_BASE = 10000.0
+SUPPORTED_HEAD_DIMS = (16, 24, 32, 64)
+
+_DTYPES = {torch.bfloat16: MPATTN_BF16, torch.float16: MPATTN_FP16, torch.float32: MPATTN_FP32}
+
+
+class MpattnError(RuntimeError):
+    """A libmpattn call returned an error code."""
+
+    def __init__(self, code, fn, detail):
+        self.code = code
+        super().__init__(f"{fn} failed ({code}: {_strerror(code)}): {detail}")
+
+
+class MpattnUnsupported(MpattnError):
+    """Valid request outside what the library implements (MPATTN_ERR_UNSUPPORTED)."""
+
+
+class Tensor4(ctypes.Structure):
+    _fields_ = [("ptr", ctypes.c_void_p), ("stride_b", ctypes.c_int64),
+                ("stride_h", ctypes.c_int64), ("stride_t", ctypes.c_int64)]
+
+
+class FwdParams(ctypes.Structure):
+    _fields_ = [
+        ("q_self", Tensor4), ("k_self", Tensor4), ("v_self", Tensor4),
+        ("q_multi", Tensor4), ("k_multi", Tensor4), ("v_multi", Tensor4),
+        ("out", Tensor4),
+        ("lse", ctypes.c_void_p),
+        ("chain_id", ctypes.c_void_p), ("chain_mask", ctypes.c_void_p),
+        ("mask_stride_b", ctypes.c_int64), ("mask_stride_q", ctypes.c_int64),
+        ("mask_stride_k", ctypes.c_int64),
+        ("key_pad", ctypes.c_void_p),
+        ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p),
+        ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("L", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("dtype", ctypes.c_int32), ("rope", ctypes.c_int32),
+        ("scale", ctypes.c_float), ("sqrt_softmax", ctypes.c_int32),
+        ("dropout_p", ctypes.c_float),
+    ]
+
+
+class BwdParams(ctypes.Structure):
+    _fields_ = [
+        ("q_self", Tensor4), ("k_self", Tensor4), ("v_self", Tensor4),
+        ("q_multi", Tensor4), ("k_multi", Tensor4), ("v_multi", Tensor4),
+        ("out", Tensor4), ("grad_out", Tensor4),
+        ("lse", ctypes.c_void_p),
+        ("dq_self", Tensor4), ("dk_self", Tensor4), ("dv_self", Tensor4),
+        ("dq_multi", Tensor4), ("dk_multi", Tensor4), ("dv_multi", Tensor4),
+        ("chain_id", ctypes.c_void_p), ("chain_mask", ctypes.c_void_p),
+        ("mask_stride_b", ctypes.c_int64), ("mask_stride_q", ctypes.c_int64),
+        ("mask_stride_k", ctypes.c_int64),
+        ("key_pad", ctypes.c_void_p),
+        ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("L", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("dtype", ctypes.c_int32), ("rope", ctypes.c_int32),
+        ("scale", ctypes.c_float), ("sqrt_softmax", ctypes.c_int32),
+    ]
+
+
+# Functions declared in include/mpattn.h, with their ctypes signatures.
+EXPORTS = {
+    "mpattn_fwd": (ctypes.c_int, [ctypes.POINTER(FwdParams), ctypes.c_void_p]),
+    "mpattn_bwd": (ctypes.c_int, [ctypes.POINTER(BwdParams), ctypes.c_void_p]),
+    "mpattn_bwd_workspace_size": (ctypes.c_int64, [ctypes.c_int32] * 4),
+    "mpattn_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+    "mpattn_last_error": (ctypes.c_char_p, []),
+    "mpattn_version": (ctypes.c_int, []),
+}
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+def load_library(path=LIB_PATH):
+    """Load libmpattn.so once; raise if it is not built."""
+    global _lib
+    with _lib_lock:
+        if _lib is None:
+            if not os.path.exists(path):
+                raise RuntimeError(
+                    f"{path} is not built: run `python -m mint_plus_amd.build` "
+                    "(or __graft_entry__.build()); there is no fallback path")
+            lib = ctypes.CDLL(path)
+            for name, (res, args) in EXPORTS.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+        return _lib
+
+
+def _strerror(code):
+    try:
+        return load_library().mpattn_strerror(code).decode()
+    except Exception:  # library absent: still produce a message
+        return "error"
+
+
+def _check(code, fn):
+    if code != MPATTN_OK:
+        detail = load_library().mpattn_last_error().decode()
+        cls = MpattnUnsupported if code == MPATTN_ERR_UNSUPPORTED else MpattnError
+        raise cls(code, fn, detail)
+
+
+def version():
+    return load_library().mpattn_version()
+
+
+def _t4(t):
+    """(B, H, L, D) view with unit head-dim stride -> Tensor4."""
+    if t is None:
+        return Tensor4(None, 0, 0, 0)
+    if t.dim() != 4:
+        raise ValueError(f"expected a 4-D (B, H, L, D) tensor, got shape {tuple(t.shape)}")
+    if t.stride(3) != 1 and t.shape[3] > 1:
+        raise ValueError("head-dim stride must be 1")
+    return Tensor4(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+_rope_cache = {}
+_rope_lock = threading.Lock()
+
+
+def rope_tables(L, D, device):
+    """Cached device cos/sin tables (L, D/2) fp32 of ``t * inv_freq``.
+
+    ``inv_freq = 1 / 10000**(arange(0, D, 2) / D)`` as in
+    mint_plus/models/rotary_embedding.py:44, rounded to fp32; the angle is
+    the fp32 product ``t * inv_freq`` (rotary_embedding.py:49-50); cos/sin are
+    evaluated in fp64 on the host and rounded to fp32 once.
+    """
+    dev = torch.device(device)
+    key = (int(L), int(D), dev.type, dev.index)
+    with _rope_lock:
+        hit = _rope_cache.get(key)
+        if hit is not None:
+            return hit
+        inv = (1.0 / ROPE_BASE ** (np.arange(0, D, 2, dtype=np.float64) / D)).astype(np.float32)
+        ang = (np.arange(L, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float64)
+        cos = torch.from_numpy(np.cos(ang).astype(np.float32)).to(dev)
+        sin = torch.from_numpy(np.sin(ang).astype(np.float32)).to(dev)
+        _rope_cache[key] = (cos, sin)
+        return cos, sin
+
+
+def _stream_handle(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _selection_args(params, chain_ids, chain_mask, key_pad, B, L, device):
+    """Fill chain_id / chain_mask / key_pad fields; returns tensors to keep alive."""
+    keep = []
+    if chain_ids is not None:
+        if tuple(chain_ids.shape) != (B, L):
+            raise ValueError(f"chain_ids must be (B, L) = {(B, L)}, got {tuple(chain_ids.shape)}")
+        cid = chain_ids.to(device=device, dtype=torch.int32).contiguous()
+        keep.append(cid)
+        params.chain_id = cid.data_ptr()
+    elif chain_mask is not None:
+        if tuple(chain_mask.shape) != (B, L, L):
+            raise ValueError(f"chain_mask must be (B, L, L) = {(B, L, L)}, got {tuple(chain_mask.shape)}")
+        cm = chain_mask
+        if cm.dtype != torch.bool and cm.dtype != torch.uint8:
+            cm = cm != 0
+        cm = cm.to(device)
+        keep.append(cm)
+        params.chain_mask = cm.data_ptr()
+        params.mask_stride_b, params.mask_stride_q, params.mask_stride_k = cm.stride()
+    else:
+        raise ValueError("one of chain_ids / chain_mask is required")
+    if key_pad is not None:
+        if tuple(key_pad.shape) != (B, L):
+            raise ValueError(f"key_padding_mask must be (B, L) = {(B, L)}, got {tuple(key_pad.shape)}")
+        kp = key_pad.to(device=device, dtype=torch.bool).contiguous()
+        keep.append(kp)
+        params.key_pad = kp.data_ptr()
+    return keep
+
+
+def _common_checks(tensors, names):
+    t0 = tensors[0]
+    if not t0.is_cuda:
+        raise RuntimeError("multi-pathway attention runs on the GPU only (inputs are on the CPU)")
+    if t0.dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {t0.dtype} (bfloat16, float16, float32)")
+    for t, n in zip(tensors, names):
+        if t.shape != t0.shape:
+            raise ValueError(f"{n} has shape {tuple(t.shape)}, expected {tuple(t0.shape)}")
+        if t.dtype != t0.dtype:
+            raise TypeError(f"{n} has dtype {t.dtype}, expected {t0.dtype}")
+        if t.device != t0.device:
+            raise ValueError(f"{n} is on {t.device}, expected {t0.device}")
+
+
+def _aligned(t):
+    """Return t, or a contiguous copy when its layout breaks the ABI's
+    16-byte row alignment rule (strides in 16-byte multiples)."""
+    q = 16 // t.element_size()
+    ok = (t.stride(3) == 1 and t.data_ptr() % 16 == 0
+          and all(s % q == 0 for s in t.stride()[:3]))
+    return t if ok else t.contiguous()
+
+
+def mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, *, chain_ids=None,
+               chain_mask=None, key_padding_mask=None, rope=False, scale=1.0,
+               sqrt_softmax=False, dropout_p=0.0, out=None, need_lse=False):
+    """Launch the forward kernel on the current stream.
+
+    Returns ``out`` (B, H, L, D) and, if ``need_lse``, the fp32 (B, H, L)
+    log-sum-exp (natural units of the scaled logits).
+    """
+    ins = [q_self, k_self, v_self, q_multi, k_multi, v_multi]
+    names = ["q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi"]
+    _common_checks(ins, names)
+    B, H, L, D = q_self.shape
+    if D not in SUPPORTED_HEAD_DIMS:
+        raise MpattnUnsupported(MPATTN_ERR_UNSUPPORTED, "mpattn_fwd",
+                                f"head dim {D} (supported: {SUPPORTED_HEAD_DIMS})")
+    ins = [_aligned(t) for t in ins]
+    dev = q_self.device
+    if out is None:
+        out = torch.empty((B, H, L, D), dtype=q_self.dtype, device=dev)
+    lse = torch.empty((B, H, L), dtype=torch.float32, device=dev) if need_lse else None
+    p = FwdParams()
+    p.q_self, p.k_self, p.v_self, p.q_multi, p.k_multi, p.v_multi = (_t4(t) for t in ins)
+    p.out = _t4(out)
+    p.lse = lse.data_ptr() if lse is not None else None
+    keep = _selection_args(p, chain_ids, chain_mask, key_padding_mask, B, L, dev)
+    if rope:
+        cos, sin = rope_tables(L, D, dev)
+        p.rope_cos, p.rope_sin = cos.data_ptr(), sin.data_ptr()
+    p.B, p.H, p.L, p.D = B, H, L, D
+    p.dtype = _DTYPES[q_self.dtype]
+    p.rope = MPATTN_ROPE_FUSED if rope else MPATTN_ROPE_NONE
+    p.scale = float(scale)
+    p.sqrt_softmax = 1 if sqrt_softmax else 0
+    p.dropout_p = float(dropout_p)
+    rc = load_library().mpattn_fwd(ctypes.byref(p), _stream_handle(dev))
+    _check(rc, "mpattn_fwd")
+    del keep, ins
+    return (out, lse) if need_lse else out
+
+
+def mpattn_bwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, out, lse, grad_out, *,
+               chain_ids=None, chain_mask=None, key_padding_mask=None, rope=False, scale=1.0,
+               sqrt_softmax=False):
+    """Launch the backward kernels; returns (dq_s, dk_s, dv_s, dq_m, dk_m, dv_m)."""
+    ins = [q_self, k_self, v_self, q_multi, k_multi, v_multi, out, grad_out]
+    names = ["q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi", "out", "grad_out"]
+    _common_checks(ins, names)
+    B, H, L, D = q_self.shape
+    if D not in SUPPORTED_HEAD_DIMS:
+        raise MpattnUnsupported(MPATTN_ERR_UNSUPPORTED, "mpattn_bwd", f"head dim {D}")
+    ins = [_aligned(t) for t in ins]
+    dev = q_self.device
+    lib = load_library()
+    grads = [torch.empty((B, H, L, D), dtype=q_self.dtype, device=dev) for _ in range(6)]
+    ws_bytes = lib.mpattn_bwd_workspace_size(B, H, L, D)
+    if ws_bytes < 0:
+        raise MpattnError(MPATTN_ERR_INVALID, "mpattn_bwd_workspace_size", "bad shape")
+    ws = torch.empty(max(1, (ws_bytes + 3) // 4), dtype=torch.float32, device=dev)
+    lse = lse.to(device=dev, dtype=torch.float32).contiguous()
+    p = BwdParams()
+    (p.q_self, p.k_self, p.v_self, p.q_multi, p.k_multi, p.v_multi, p.out,
+     p.grad_out) = (_t4(t) for t in ins)
+    p.lse = lse.data_ptr()
+    (p.dq_self, p.dk_self, p.dv_self, p.dq_multi, p.dk_multi, p.dv_multi) = (_t4(g) for g in grads)
+    keep = _selection_args(p, chain_ids, chain_mask, key_padding_mask, B, L, dev)
+    if rope:
+        cos, sin = rope_tables(L, D, dev)
+        p.rope_cos, p.rope_sin = cos.data_ptr(), sin.data_ptr()
+    p.workspace = ws.data_ptr()
+    p.B, p.H, p.L, p.D = B, H, L, D
+    p.dtype = _DTYPES[q_self.dtype]
+    p.rope = MPATTN_ROPE_FUSED if rope else MPATTN_ROPE_NONE
+    p.scale = float(scale)
+    p.sqrt_softmax = 1 if sqrt_softmax else 0
+    rc = lib.mpattn_bwd(ctypes.byref(p), _stream_handle(dev))
+    _check(rc, "mpattn_bwd")
+    del keep, ins
+    return tuple(grads)
+
+
+def default_scale(D):
+    return D ** -0.5 if D > 0 else 1.0
+
+
+__all__ = ["mpattn_fwd", "mpattn_bwd", "load_library", "rope_tables", "version",
+           "MpattnError", "MpattnUnsupported", "EXPORTS", "LIB_PATH", "default_scale"]

@@ -1,0 +1,152 @@
+// C-ABI entry points of libmpattn.so: argument validation and dispatch.
+//
+// Validation mirrors the reference wrappers' asserts
+// (mint_plus/models/kernels/multi_pathway_attention.py:224-227,
+// mint_plus/models/kernels/__init__.py:203) and adds the layout rules the
+// vectorised kernels rely on (16-byte aligned rows).
+#include <stdarg.h>
+#include <stdio.h>
+#include <math.h>
+
+#include "mpattn_common.h"
+
+namespace mpattn {
+hipError_t launch_fwd16(const mpattn_fwd_params& p, hipStream_t stream);
+hipError_t launch_fwd32(const mpattn_fwd_params& p, hipStream_t stream);
+hipError_t launch_bwd(const mpattn_bwd_params& p, hipStream_t stream);
+int64_t bwd_workspace_bytes(int B, int H, int L, int D);
+}  // namespace mpattn
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int elt_size(int dtype) { return dtype == MPATTN_FP32 ? 4 : 2; }
+
+// Every row start must be 16-byte aligned: base pointer aligned and all
+// strides multiples of 16 bytes.
+int check_tensor(const mpattn_tensor& t, const char* name, int esize, bool out) {
+    if (!t.ptr) return fail(MPATTN_ERR_INVALID, "%s: null pointer", name);
+    if ((uintptr_t)t.ptr % 16) return fail(MPATTN_ERR_UNSUPPORTED, "%s: base not 16-byte aligned", name);
+    const int64_t q = 16 / esize;
+    if (t.stride_b % q || t.stride_h % q || t.stride_t % q)
+        return fail(MPATTN_ERR_UNSUPPORTED, "%s: strides must be multiples of %lld elements", name,
+                    (long long)q);
+    if (t.stride_b < 0 || t.stride_h < 0 || t.stride_t < 0)
+        return fail(MPATTN_ERR_UNSUPPORTED, "%s: negative stride", name);
+    (void)out;
+    return MPATTN_OK;
+}
+
+int check_common(int B, int H, int L, int D, int dtype, int rope, float scale,
+                 const int32_t* chain_id, const uint8_t* chain_mask, int64_t msb, int64_t msq,
+                 int64_t msk, const float* rc, const float* rs, int sqrt_softmax) {
+    if (B < 1 || H < 1 || L < 1) return fail(MPATTN_ERR_INVALID, "B, H, L must be >= 1 (got %d, %d, %d)", B, H, L);
+    if (dtype != MPATTN_BF16 && dtype != MPATTN_FP16 && dtype != MPATTN_FP32)
+        return fail(MPATTN_ERR_INVALID, "unknown dtype %d", dtype);
+    if (D != 16 && D != 24 && D != 32 && D != 64)
+        return fail(MPATTN_ERR_UNSUPPORTED, "head dim %d not supported (16, 24, 32, 64)", D);
+    if (rope != MPATTN_ROPE_NONE && rope != MPATTN_ROPE_FUSED)
+        return fail(MPATTN_ERR_INVALID, "unknown rope mode %d", rope);
+    if (!(scale > 0.f) || !isfinite(scale)) return fail(MPATTN_ERR_INVALID, "scale must be finite and > 0");
+    if ((chain_id == nullptr) == (chain_mask == nullptr))
+        return fail(MPATTN_ERR_INVALID, "exactly one of chain_id / chain_mask must be given");
+    if (chain_id && (uintptr_t)chain_id % 4) return fail(MPATTN_ERR_INVALID, "chain_id misaligned");
+    if (chain_mask && (msb < 0 || msq < 0 || msk < 0))
+        return fail(MPATTN_ERR_UNSUPPORTED, "chain_mask: negative stride");
+    if (rope == MPATTN_ROPE_FUSED) {
+        if (!rc || !rs) return fail(MPATTN_ERR_INVALID, "rope tables required for fused RoPE");
+        if ((uintptr_t)rc % 16 || (uintptr_t)rs % 16)
+            return fail(MPATTN_ERR_UNSUPPORTED, "rope tables not 16-byte aligned");
+    }
+    if (sqrt_softmax != 0 && sqrt_softmax != 1) return fail(MPATTN_ERR_INVALID, "sqrt_softmax must be 0/1");
+    const int64_t nblk = (int64_t)B * H * ((L + 127) / 128);
+    if (nblk > 0x7fffffffLL || (int64_t)L * 4 > 0x7fffffffLL)
+        return fail(MPATTN_ERR_UNSUPPORTED, "problem too large for one launch");
+    return MPATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mpattn_version(void) { return MPATTN_VERSION; }
+
+const char* mpattn_last_error(void) { return g_last_error; }
+
+const char* mpattn_strerror(int code) {
+    switch (code) {
+        case MPATTN_OK: return "success";
+        case MPATTN_ERR_INVALID: return "invalid argument";
+        case MPATTN_ERR_UNSUPPORTED: return "unsupported configuration";
+        case MPATTN_ERR_LAUNCH: return "kernel launch failed";
+    }
+    return "unknown error";
+}
+
+int mpattn_fwd(const mpattn_fwd_params* p, void* stream) {
+    g_last_error[0] = 0;
+    if (!p) return fail(MPATTN_ERR_INVALID, "null params");
+    int rc = check_common(p->B, p->H, p->L, p->D, p->dtype, p->rope, p->scale, p->chain_id,
+                          p->chain_mask, p->mask_stride_b, p->mask_stride_q, p->mask_stride_k,
+                          p->rope_cos, p->rope_sin, p->sqrt_softmax);
+    if (rc) return rc;
+    if (p->dropout_p != 0.f)
+        return fail(MPATTN_ERR_UNSUPPORTED, "dropout_p must be 0 (got %g)", (double)p->dropout_p);
+    const int es = elt_size(p->dtype);
+    const mpattn_tensor* ts[7] = {&p->q_self, &p->k_self, &p->v_self, &p->q_multi,
+                                  &p->k_multi, &p->v_multi, &p->out};
+    const char* names[7] = {"q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi", "out"};
+    for (int i = 0; i < 7; ++i)
+        if ((rc = check_tensor(*ts[i], names[i], es, i == 6))) return rc;
+    if (p->lse && (uintptr_t)p->lse % 4) return fail(MPATTN_ERR_INVALID, "lse misaligned");
+    hipError_t e;
+    if (p->dtype == MPATTN_FP32) {
+        e = mpattn::launch_fwd32(*p, (hipStream_t)stream);
+    } else {
+        if (p->sqrt_softmax) return fail(MPATTN_ERR_UNSUPPORTED, "sqrt_softmax not built for 16-bit yet");
+        e = mpattn::launch_fwd16(*p, (hipStream_t)stream);
+    }
+    if (e != hipSuccess) return fail(MPATTN_ERR_LAUNCH, "fwd launch: %s", hipGetErrorString(e));
+    return MPATTN_OK;
+}
+
+int64_t mpattn_bwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D) {
+    if (B < 1 || H < 1 || L < 1) return -1;
+    return mpattn::bwd_workspace_bytes(B, H, L, D);
+}
+
+int mpattn_bwd(const mpattn_bwd_params* p, void* stream) {
+    g_last_error[0] = 0;
+    if (!p) return fail(MPATTN_ERR_INVALID, "null params");
+    int rc = check_common(p->B, p->H, p->L, p->D, p->dtype, p->rope, p->scale, p->chain_id,
+                          p->chain_mask, p->mask_stride_b, p->mask_stride_q, p->mask_stride_k,
+                          p->rope_cos, p->rope_sin, p->sqrt_softmax);
+    if (rc) return rc;
+    const int es = elt_size(p->dtype);
+    const mpattn_tensor* ts[14] = {&p->q_self,  &p->k_self,   &p->v_self,  &p->q_multi, &p->k_multi,
+                                   &p->v_multi, &p->out,      &p->grad_out, &p->dq_self, &p->dk_self,
+                                   &p->dv_self, &p->dq_multi, &p->dk_multi, &p->dv_multi};
+    const char* names[14] = {"q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi", "out",
+                             "grad_out", "dq_self", "dk_self", "dv_self", "dq_multi", "dk_multi",
+                             "dv_multi"};
+    for (int i = 0; i < 14; ++i)
+        if ((rc = check_tensor(*ts[i], names[i], es, i >= 8))) return rc;
+    if (!p->lse || (uintptr_t)p->lse % 4) return fail(MPATTN_ERR_INVALID, "lse required (fp32, aligned)");
+    if (!p->workspace || (uintptr_t)p->workspace % 16)
+        return fail(MPATTN_ERR_INVALID, "workspace required (16-byte aligned)");
+    hipError_t e = mpattn::launch_bwd(*p, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return fail(MPATTN_ERR_UNSUPPORTED, "bwd: configuration not built");
+    if (e != hipSuccess) return fail(MPATTN_ERR_LAUNCH, "bwd launch: %s", hipGetErrorString(e));
+    return MPATTN_OK;
+}
+
+}  // extern "C"

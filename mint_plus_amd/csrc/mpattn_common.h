@@ -1,0 +1,170 @@
+// Shared device helpers for the gfx950 multi-pathway attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mpattn.h"
+
+namespace mpattn {
+
+typedef __bf16 bf16_t;
+typedef _Float16 fp16_t;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 fp16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 fp16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 fp16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Marks a padded key in the per-tile chain-id staging buffers. Real chain ids
+// must be larger than this value.
+constexpr int kPadChain = INT32_MIN;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// 16-bit element traits: the 8-wide MFMA operand vector and the
+// 32x32x16 MFMA (gfx950) that consumes it.
+template <typename T> struct Elt;
+
+template <> struct Elt<bf16_t> {
+    typedef bf16x8 v8;
+    typedef bf16x4 v4;
+    typedef bf16x2 v2;
+    static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <> struct Elt<fp16_t> {
+    typedef fp16x8 v8;
+    typedef fp16x4 v4;
+    typedef fp16x2 v2;
+    static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+__device__ __forceinline__ float fast_exp2(float x) {
+    return __builtin_amdgcn_exp2f(x);
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup i runs on
+// XCD i % 8). Remap so each XCD receives one contiguous range of logical ids:
+// neighbouring logical ids (query blocks of the same (b, h)) then share an
+// L2 and reuse each other's K/V tiles.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+    constexpr int kXcd = 8;
+    const int xcd = bid % kXcd, slot = bid / kXcd;
+    const int per = nblocks / kXcd, rem = nblocks % kXcd;
+    return xcd * per + (xcd < rem ? xcd : rem) + slot;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Reductions inside each 32-lane half of a wave.
+__device__ __forceinline__ int half_min_i(int v) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ int half_max_i(int v) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o));
+    return v;
+}
+
+// 8 consecutive elements of a row, widened to fp32. `d0` is a multiple of 8.
+template <typename T>
+__device__ __forceinline__ void load8f(const T* row, int d0, float out[8]) {
+    typedef typename Elt<T>::v8 v8;
+    const v8 x = *reinterpret_cast<const v8*>(row + d0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) out[t] = (float)x[t];
+}
+
+// 8 elements [d0, d0+8) of RoPE(row) * mul at position `pos`, for head dim D
+// (half-split layout: dim d pairs with d +- D/2; emb = cat(freqs, freqs)).
+// Dims >= D read as 0.
+template <typename T, int D>
+__device__ __forceinline__ void load8_rot(const T* row, const float* cos_tab,
+                                          const float* sin_tab, int pos, int d0,
+                                          float mul, bool rope, float out[8]) {
+    constexpr int H2 = D / 2;
+    if (d0 >= D) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) out[t] = 0.f;
+        return;
+    }
+    float x[8];
+    load8f<T>(row, d0, x);
+    if (!rope) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) out[t] = x[t] * mul;
+        return;
+    }
+    const float* cr = cos_tab + (int64_t)pos * H2;
+    const float* sr = sin_tab + (int64_t)pos * H2;
+    if constexpr (H2 % 8 == 0) {
+        // The whole 8-chunk lies on one side of D/2: one partner chunk.
+        const bool lo = d0 < H2;
+        const int dp = lo ? d0 + H2 : d0 - H2;
+        const int fi = lo ? d0 : dp;
+        float y[8];
+        load8f<T>(row, dp, y);
+        const f32x4 c0 = *reinterpret_cast<const f32x4*>(cr + fi);
+        const f32x4 c1 = *reinterpret_cast<const f32x4*>(cr + fi + 4);
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(sr + fi);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(sr + fi + 4);
+        const float sg = lo ? -1.f : 1.f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float c = t < 4 ? c0[t & 3] : c1[t & 3];
+            const float s = t < 4 ? s0[t & 3] : s1[t & 3];
+            out[t] = (x[t] * c + sg * y[t] * s) * mul;
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int d = d0 + t;
+            const bool lo = d < H2;
+            const int dp = lo ? d + H2 : d - H2;
+            const int fi = lo ? d : dp;
+            const float y = (float)row[dp];
+            const float sg = lo ? -1.f : 1.f;
+            out[t] = (x[t] * cr[fi] + sg * y * sr[fi]) * mul;
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ typename Elt<T>::v8 pack8(const float x[8]) {
+    typename Elt<T>::v8 r;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) r[t] = (T)x[t];
+    return r;
+}
+
+}  // namespace mpattn

@@ -1,0 +1,15 @@
+"""gfx950 kernels of the multi-pathway attention op, with the reference's
+Python entry points (``mint_plus/models/kernels/__init__.py``,
+``multi_pathway_attention.py``, ``multi_pathway_attention_bwd.py``,
+``multi_pathway_attention_fp16.py``, ``differentiable_attention.py``)."""
+from .multi_pathway_attention import (fused_multi_pathway_attention,
+                                      fused_multi_pathway_attention_fp16)
+from .multi_pathway_attention_bwd import fused_multi_pathway_attention_bwd
+from .differentiable_attention import differentiable_multi_pathway_attention
+
+__all__ = [
+    "fused_multi_pathway_attention",
+    "fused_multi_pathway_attention_fp16",
+    "fused_multi_pathway_attention_bwd",
+    "differentiable_multi_pathway_attention",
+]

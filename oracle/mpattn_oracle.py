@@ -1,0 +1,217 @@
+"""CPU oracle for multi-pathway attention -- TEST INFRASTRUCTURE ONLY.
+
+This module is the checker, never the product: only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+it. The HIP library (``mint_plus_amd``) never calls into it.
+
+It restates, in float64 numpy, the math of the reference's eager path:
+
+* RoPE -- ``mint_plus/models/rotary_embedding.py:16-55``: half-split layout,
+  ``inv_freq = 1 / 10000**(arange(0, D, 2) / D)``, global positions
+  ``t = arange(L)``, ``emb = cat(freqs, freqs)``,
+  ``x*cos + rotate_half(x)*sin`` with ``rotate_half = cat(-x2, x1)``.
+* Logits -- ``mint_plus/models/attention.py:186-236`` (self pathway: scale,
+  RoPE, bmm, key padding -> -inf) and ``:343-365`` (multimer pathway: scale,
+  bmm, key padding, no RoPE).
+* Combine -- ``mint_plus/models/modules_plus.py:178-194``:
+  ``where(chain_mask, inter, intra)``, one softmax over all keys, split by
+  pathway, ``P_intra @ V_self + P_inter @ V_multi``. The softmax runs in high
+  precision as in ``mint_plus/models/mu_scaling/layer.py:159`` and
+  ``profiles/test_sqrt_softmax.py:77-94`` (the eager bf16 softmax of
+  ``modules_plus.py:185`` is a reference quirk, not a target).
+* A row whose keys are all padded gives 0, the ``d == 0`` guard of
+  ``mint_plus/models/kernels/multi_pathway_attention.py:163-167``.
+* ``sqrt_softmax``: ``O = sum_j sqrt(P_ij) V_j``
+  (``multi_pathway_attention.py:138-152,164-165``).
+
+Gradients are analytic (softmax backward ``dS = P * (dP - rowsum(P*dP))``
+and the transpose of the RoPE rotation). The reference's Triton backward
+(``multi_pathway_attention_bwd.py``) is not followed: it is mathematically
+wrong (see the module tests, which pin these gradients by central finite
+differences instead).
+
+How each function is pinned (``tests/test_oracle.py``):
+
+* ``rope_tables`` / ``apply_rope``: identity at position 0, norm
+  preservation, the relative-position identity
+  ``<R_i q, R_j k> = <q, R_{j-i} k>``, and a hand-computed half-split vector.
+* ``mpattn_forward``: reduction to ``torch.nn.functional.scaled_dot_product_attention``
+  on concatenated features (one call per query chain), all-same-chain
+  reduction to plain SDPA with RoPE, invariants (chain-label permutation,
+  appended padded keys, constant V, zero Q), L = 1, and a pure-Python
+  triple loop on tiny inputs.
+* ``mpattn_backward``: central finite differences of ``mpattn_forward``.
+"""
+import numpy as np
+
+ROPE_BASE = 10000.0
+
+
+def rope_tables(L, D):
+    """cos/sin tables (L, D/2) of the angle ``t * inv_freq[i]``.
+
+    Follows ``rotary_embedding.py:44,49-53``: ``inv_freq`` and the angle
+    ``t * inv_freq`` are fp32 quantities in the reference, so they are formed
+    here in fp32 (inv_freq = fp32 rounding of the exact value, angle = one
+    fp32 product); cos/sin are then evaluated in fp64.
+    """
+    inv = (1.0 / ROPE_BASE ** (np.arange(0, D, 2, dtype=np.float64) / D)).astype(np.float32)
+    t = np.arange(L, dtype=np.float32)
+    ang = (t[:, None] * inv[None, :]).astype(np.float64)  # fp32 product, exact in fp64
+    return np.cos(ang), np.sin(ang)
+
+
+def apply_rope(x, cos, sin):
+    """``x * cos + rotate_half(x) * sin`` on (..., L, D), positions 0..L-1
+    (``rotary_embedding.py:16-24``)."""
+    h = x.shape[-1] // 2
+    x1, x2 = x[..., :h], x[..., h:]
+    return np.concatenate([x1 * cos - x2 * sin, x2 * cos + x1 * sin], axis=-1)
+
+
+def apply_rope_transpose(g, cos, sin):
+    """Transpose of ``apply_rope`` (rotation by the negative angle)."""
+    h = g.shape[-1] // 2
+    g1, g2 = g[..., :h], g[..., h:]
+    return np.concatenate([g1 * cos + g2 * sin, g2 * cos - g1 * sin], axis=-1)
+
+
+def cross_mask(chain_ids=None, chain_mask=None):
+    """(B, L, L) bool, True where query and key are on different chains
+    (``esm2.py:89``: ``~eq(chain_ids[:, :, None], chain_ids[:, None, :])``)."""
+    if chain_mask is not None:
+        return np.asarray(chain_mask, dtype=bool)
+    c = np.asarray(chain_ids)
+    return c[:, :, None] != c[:, None, :]
+
+
+def _prepare(qs, ks, qm, km, rope, scale):
+    qs, ks, qm, km = (np.asarray(a, dtype=np.float64) for a in (qs, ks, qm, km))
+    L, D = qs.shape[-2], qs.shape[-1]
+    if rope:
+        cos, sin = rope_tables(L, D)
+        qs_r, ks_r = apply_rope(qs, cos, sin), apply_rope(ks, cos, sin)
+    else:
+        cos = sin = None
+        qs_r, ks_r = qs, ks
+    s_self = scale * np.einsum("bhid,bhjd->bhij", qs_r, ks_r)
+    s_multi = scale * np.einsum("bhid,bhjd->bhij", qm, km)
+    return qs_r, ks_r, s_self, s_multi, cos, sin
+
+
+def _probs(s_self, s_multi, cross, key_pad):
+    s = np.where(cross[:, None], s_multi, s_self)
+    if key_pad is not None:
+        s = np.where(np.asarray(key_pad, dtype=bool)[:, None, None, :], -np.inf, s)
+    m = s.max(axis=-1, keepdims=True)
+    dead = ~np.isfinite(m)  # every key padded
+    m = np.where(dead, 0.0, m)
+    e = np.exp(s - m)
+    l = e.sum(axis=-1, keepdims=True)
+    p = np.where(l > 0, e / np.where(l > 0, l, 1.0), 0.0)
+    lse = np.where(l[..., 0] > 0, m[..., 0] + np.log(np.where(l[..., 0] > 0, l[..., 0], 1.0)), -np.inf)
+    return p, lse
+
+
+def mpattn_forward(qs, ks, vs, qm, km, vm, chain_ids=None, chain_mask=None, key_pad=None,
+                   rope=False, scale=1.0, sqrt_softmax=False):
+    """Multi-pathway attention forward in float64.
+
+    Inputs (B, H, L, D); ``chain_ids`` (B, L) or ``chain_mask`` (B, L, L)
+    (True = different chains); ``key_pad`` (B, L) bool (True = padded key).
+    ``rope`` applies RoPE to q_self/k_self; ``scale`` multiplies both logits.
+    Returns ``(out (B,H,L,D), lse (B,H,L))``; lse is in natural-log units.
+    """
+    cross = cross_mask(chain_ids, chain_mask)
+    _, _, s_self, s_multi, _, _ = _prepare(qs, ks, qm, km, rope, scale)
+    p, lse = _probs(s_self, s_multi, cross, key_pad)
+    w = np.sqrt(p) if sqrt_softmax else p
+    c = cross[:, None]
+    vs, vm = np.asarray(vs, np.float64), np.asarray(vm, np.float64)
+    out = np.einsum("bhij,bhjd->bhid", np.where(c, 0.0, w), vs) + \
+        np.einsum("bhij,bhjd->bhid", np.where(c, w, 0.0), vm)
+    return out, lse
+
+
+def mpattn_backward(qs, ks, vs, qm, km, vm, grad_out, chain_ids=None, chain_mask=None,
+                    key_pad=None, rope=False, scale=1.0, sqrt_softmax=False):
+    """Gradients (dq_s, dk_s, dv_s, dq_m, dk_m, dv_m) of
+    ``sum(grad_out * mpattn_forward(...)[0])`` in float64."""
+    cross = cross_mask(chain_ids, chain_mask)
+    qs_r, ks_r, s_self, s_multi, cos, sin = _prepare(qs, ks, qm, km, rope, scale)
+    qm, km = np.asarray(qm, np.float64), np.asarray(km, np.float64)
+    vs, vm = np.asarray(vs, np.float64), np.asarray(vm, np.float64)
+    g = np.asarray(grad_out, np.float64)
+    p, _ = _probs(s_self, s_multi, cross, key_pad)
+    c = cross[:, None]
+    w = np.sqrt(p) if sqrt_softmax else p
+    w_s, w_m = np.where(c, 0.0, w), np.where(c, w, 0.0)
+    dv_s = np.einsum("bhij,bhid->bhjd", w_s, g)
+    dv_m = np.einsum("bhij,bhid->bhjd", w_m, g)
+    # dW_ij = dO_i . V_sel(ij), j
+    dw = np.where(c, np.einsum("bhid,bhjd->bhij", g, vm), np.einsum("bhid,bhjd->bhij", g, vs))
+    if sqrt_softmax:
+        # W = sqrt(P): P * dP = W * dW / 2
+        pdp = 0.5 * w * dw
+    else:
+        pdp = p * dw
+    ds = pdp - p * pdp.sum(axis=-1, keepdims=True)
+    ds_s, ds_m = np.where(c, 0.0, ds), np.where(c, ds, 0.0)
+    dq_s = scale * np.einsum("bhij,bhjd->bhid", ds_s, ks_r)
+    dk_s = scale * np.einsum("bhij,bhid->bhjd", ds_s, qs_r)
+    dq_m = scale * np.einsum("bhij,bhjd->bhid", ds_m, km)
+    dk_m = scale * np.einsum("bhij,bhid->bhjd", ds_m, qm)
+    if rope:
+        dq_s = apply_rope_transpose(dq_s, cos, sin)
+        dk_s = apply_rope_transpose(dk_s, cos, sin)
+    return dq_s, dk_s, dv_s, dq_m, dk_m, dv_m
+
+
+def mpattn_forward_loops(qs, ks, vs, qm, km, vm, chain_ids, key_pad=None, rope=False, scale=1.0):
+    """Pure-Python triple loop of the same forward, for tiny inputs only.
+
+    Written element by element from the definition (rotation of each pair
+    (d, d + D/2), logit selection per (i, j), max-subtracted softmax), as an
+    independent cross-check of the vectorised ``mpattn_forward``.
+    """
+    import math
+    B, H, L, D = len(qs), len(qs[0]), len(qs[0][0]), len(qs[0][0][0])
+    half = D // 2
+
+    def rot(x, pos):
+        if not rope:
+            return list(x)
+        y = [0.0] * D
+        for i in range(half):
+            inv = float(np.float32(1.0 / ROPE_BASE ** (2 * i / D)))
+            a = float(np.float32(np.float32(pos) * np.float32(inv)))
+            y[i] = x[i] * math.cos(a) - x[i + half] * math.sin(a)
+            y[i + half] = x[i + half] * math.cos(a) + x[i] * math.sin(a)
+        return y
+
+    out = [[[[0.0] * D for _ in range(L)] for _ in range(H)] for _ in range(B)]
+    for b in range(B):
+        for h in range(H):
+            kr = [rot(ks[b][h][j], j) for j in range(L)]
+            for i in range(L):
+                qr = rot(qs[b][h][i], i)
+                logits, vals = [], []
+                for j in range(L):
+                    if key_pad is not None and key_pad[b][j]:
+                        continue
+                    if chain_ids[b][i] == chain_ids[b][j]:
+                        s = scale * sum(qr[d] * kr[j][d] for d in range(D))
+                        v = vs[b][h][j]
+                    else:
+                        s = scale * sum(qm[b][h][i][d] * km[b][h][j][d] for d in range(D))
+                        v = vm[b][h][j]
+                    logits.append(s)
+                    vals.append(v)
+                if not logits:
+                    continue
+                mx = max(logits)
+                e = [math.exp(s - mx) for s in logits]
+                tot = sum(e)
+                for d in range(D):
+                    out[b][h][i][d] = sum(e[j] * vals[j][d] for j in range(len(e))) / tot
+    return np.array(out)

@@ -1,0 +1,203 @@
+"""Forward parity of the HIP kernel (through the C ABI) against the oracle.
+
+Tolerances (stated by the task for this op):
+  bf16 / fp16 inputs: |gpu - ref| <= 2e-2 + 1e-2 * |ref|, ref in float64/fp32
+  fp32 inputs:        max |gpu - ref| <= 1e-4
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import multi_chain_ids, tail_padding, two_chain_ids
+from oracle import mpattn_oracle as orc
+from oracle import torch_ref
+
+pytestmark = pytest.mark.gpu
+
+ATOL16, RTOL16 = 2e-2, 1e-2
+ATOL32 = 1e-4
+DEV = "cuda:0"
+
+
+def _mpattn():
+    import mint_plus_amd
+    return mint_plus_amd
+
+
+def make_inputs(B, H, L, D, dtype, seed, sigma=None, nchains=2, pad=True):
+    rng = np.random.default_rng(seed)
+    sigma = D ** -0.5 if sigma is None else sigma
+    xs = [torch.from_numpy(rng.standard_normal((B, H, L, D)).astype(np.float32) * sigma)
+          for _ in range(6)]
+    xs = [x.to(dtype) for x in xs]
+    if nchains == 2:
+        cid = two_chain_ids(rng, B, L)
+    else:
+        cid = multi_chain_ids(rng, B, L, nchains)
+    kp = tail_padding(rng, B, L) if pad else np.zeros((B, L), dtype=bool)
+    return xs, cid, kp
+
+
+def run_gpu(xs, cid, kp, rope, scale, dtype_out=None, dense=False):
+    m = _mpattn()
+    g = [x.to(DEV) for x in xs]
+    kw = dict(key_padding_mask=torch.from_numpy(kp).to(DEV), rope=rope, scale=scale)
+    if dense:
+        c = torch.from_numpy(cid)
+        cm = (c[:, :, None] != c[:, None, :]).to(DEV)
+        out = m.fused_multi_pathway_attention(*g, cm, training=False, **kw)
+    else:
+        out = m.fused_multi_pathway_attention(*g, None, training=False,
+                                              chain_ids=torch.from_numpy(cid).to(DEV), **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy().astype(np.float64)
+
+
+def oracle_out(xs, cid, kp, rope, scale):
+    a = [x.double().numpy() for x in xs]
+    out, _ = orc.mpattn_forward(*a, chain_ids=cid, key_pad=kp, rope=rope, scale=scale)
+    return out
+
+
+def assert_close16(got, ref, what):
+    err = np.abs(got - ref)
+    bound = ATOL16 + RTOL16 * np.abs(ref)
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {bad.sum()} elements out of tolerance; "
+                           f"max err {err.max():.4g}, worst excess {(err - bound).max():.4g}")
+
+
+@pytest.mark.parametrize("D", [16, 24, 32, 64])
+@pytest.mark.parametrize("L", [64, 100, 257])
+def test_fwd_bf16_small(D, L):
+    print(f"[fwd bf16] D={D} L={L}", flush=True)
+    xs, cid, kp = make_inputs(2, 3, L, D, torch.bfloat16, seed=1000 + D + L)
+    got = run_gpu(xs, cid, kp, rope=True, scale=D ** -0.5)
+    ref = oracle_out(xs, cid, kp, rope=True, scale=D ** -0.5)
+    assert_close16(got, ref, f"bf16 D={D} L={L}")
+
+
+def prerotate(xs, D, scale, dtype=torch.bfloat16):
+    """The reference's caller-side contract: q scaled, q/k of the self pathway
+    rotated, all rounded to the input dtype (modules_plus.py:125-135)."""
+    L = xs[0].shape[2]
+    cos, sin = orc.rope_tables(L, D)
+    a = [x.double().numpy() for x in xs]
+    qs = orc.apply_rope(a[0], cos, sin) * scale
+    ks = orc.apply_rope(a[1], cos, sin)
+    qm = a[3] * scale
+    cast = lambda v: torch.from_numpy(v).to(dtype)
+    return [cast(qs), cast(ks), xs[2], cast(qm), xs[4], xs[5]]
+
+
+@pytest.mark.parametrize("D", [16, 32, 64])
+def test_fwd_sharp_logits(D):
+    """Large logits (sigma 2, logits up to ~15): exercises the lazy-rescale
+    path. Inputs are pre-rotated and rounded on the host so the oracle sees
+    exactly the operands the MFMAs see (with fused RoPE the bf16 rounding of
+    the rotated q/k alone moves logits of this size by ~0.1)."""
+    print(f"[fwd sharp] D={D}", flush=True)
+    xs, cid, kp = make_inputs(2, 2, 300, D, torch.bfloat16, seed=7 + D, sigma=2.0)
+    pre = prerotate(xs, D, D ** -0.5)
+    got = run_gpu(pre, cid, kp, rope=False, scale=1.0)
+    ref = oracle_out(pre, cid, kp, rope=False, scale=1.0)
+    assert_close16(got, ref, f"sharp D={D}")
+
+
+@pytest.mark.parametrize("nchains", [1, 3, 5])
+def test_fwd_chain_counts(nchains):
+    print(f"[fwd chains] n={nchains}", flush=True)
+    xs, cid, kp = make_inputs(2, 2, 333, 32, torch.bfloat16, seed=50 + nchains, nchains=nchains)
+    got = run_gpu(xs, cid, kp, rope=True, scale=32 ** -0.5)
+    ref = oracle_out(xs, cid, kp, rope=True, scale=32 ** -0.5)
+    assert_close16(got, ref, f"nchains={nchains}")
+
+
+def test_fwd_prerotated_contract():
+    """Reference contract: q pre-scaled, q/k pre-rotated, scale 1, dense mask."""
+    print("[fwd prerotated dense]", flush=True)
+    D, L = 32, 200
+    xs, cid, kp = make_inputs(2, 2, L, D, torch.bfloat16, seed=3, pad=False)
+    pre = prerotate(xs, D, D ** -0.5)
+    got = run_gpu(pre, cid, kp, rope=False, scale=1.0, dense=True)
+    ref = oracle_out(pre, cid, kp, rope=False, scale=1.0)
+    assert_close16(got, ref, "prerotated dense")
+
+
+def test_fwd_fp16():
+    print("[fwd fp16]", flush=True)
+    xs, cid, kp = make_inputs(2, 3, 190, 32, torch.float16, seed=11)
+    got = run_gpu(xs, cid, kp, rope=True, scale=32 ** -0.5)
+    ref = oracle_out(xs, cid, kp, rope=True, scale=32 ** -0.5)
+    assert_close16(got, ref, "fp16")
+
+
+def test_fwd_headline_shape():
+    """150M shape (B=16, H=20, L=1024, D=32, bf16) vs a chunked fp32 reference."""
+    print("[fwd headline 16x20x1024x32]", flush=True)
+    B, H, L, D = 16, 20, 1024, 32
+    xs, cid, kp = make_inputs(B, H, L, D, torch.bfloat16, seed=2024)
+    g = [x.to(DEV) for x in xs]
+    cid_t = torch.from_numpy(cid).to(DEV)
+    kp_t = torch.from_numpy(kp).to(DEV)
+    m = _mpattn()
+    out = m.fused_multi_pathway_attention(*g, None, training=False, chain_ids=cid_t,
+                                          key_padding_mask=kp_t, rope=True, scale=D ** -0.5)
+    ref, _ = torch_ref.forward(*g, chain_ids=cid_t, key_pad=kp_t, rope=True, scale=D ** -0.5,
+                               dtype=torch.float32, chunk=2)
+    err = (out.float() - ref).abs()
+    bound = ATOL16 + RTOL16 * ref.abs()
+    assert bool((err <= bound).all()), f"max err {err.max().item():.4g}"
+
+
+def test_fwd_lse():
+    """The log-sum-exp the forward saves for the backward."""
+    print("[fwd lse]", flush=True)
+    D, L = 32, 150
+    xs, cid, kp = make_inputs(2, 2, L, D, torch.bfloat16, seed=5)
+    m = _mpattn()
+    g = [x.to(DEV) for x in xs]
+    _, lse = m._lib.mpattn_fwd(*g, chain_ids=torch.from_numpy(cid).to(DEV),
+                               key_padding_mask=torch.from_numpy(kp).to(DEV), rope=True,
+                               scale=D ** -0.5, need_lse=True)
+    a = [x.double().numpy() for x in xs]
+    _, lse_ref = orc.mpattn_forward(*a, chain_ids=cid, key_pad=kp, rope=True, scale=D ** -0.5)
+    np.testing.assert_allclose(lse.cpu().numpy(), lse_ref, atol=2e-2, rtol=1e-3)
+
+
+def test_fwd_all_keys_padded_row():
+    """A sample whose keys are all padded outputs zeros (d == 0 guard)."""
+    print("[fwd all padded]", flush=True)
+    D, L = 32, 96
+    xs, cid, kp = make_inputs(2, 2, L, D, torch.bfloat16, seed=9, pad=False)
+    kp[1, :] = True
+    got = run_gpu(xs, cid, kp, rope=True, scale=D ** -0.5)
+    ref = oracle_out(xs, cid, kp, rope=True, scale=D ** -0.5)
+    assert np.all(got[1] == 0.0)
+    assert_close16(got, ref, "all padded")
+
+
+def test_fwd_strided_views():
+    """Q/K/V read straight from a (L, B, 3E) projection output via strides."""
+    print("[fwd strided]", flush=True)
+    B, H, L, D = 2, 4, 130, 32
+    E = H * D
+    rng = np.random.default_rng(21)
+    qkv_s = torch.from_numpy(rng.standard_normal((L, B, 3 * E)).astype(np.float32) * 0.2).to(torch.bfloat16)
+    qkv_m = torch.from_numpy(rng.standard_normal((L, B, 3 * E)).astype(np.float32) * 0.2).to(torch.bfloat16)
+
+    def views(qkv):
+        q, k, v = qkv.chunk(3, dim=-1)
+        return [t.view(L, B, H, D).permute(1, 2, 0, 3) for t in (q, k, v)]
+
+    cid = two_chain_ids(rng, B, L)
+    kp = tail_padding(rng, B, L)
+    dv = [v for v in views(qkv_s.to(DEV))] + [v for v in views(qkv_m.to(DEV))]
+    m = _mpattn()
+    out = m.fused_multi_pathway_attention(*dv, None, training=False,
+                                          chain_ids=torch.from_numpy(cid).to(DEV),
+                                          key_padding_mask=torch.from_numpy(kp).to(DEV),
+                                          rope=True, scale=D ** -0.5)
+    host = [t.contiguous() for t in views(qkv_s)] + [t.contiguous() for t in views(qkv_m)]
+    ref = oracle_out(host, cid, kp, rope=True, scale=D ** -0.5)
+    assert_close16(out.float().cpu().numpy(), ref, "strided")
