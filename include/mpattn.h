@@ -91,6 +91,9 @@ typedef struct mpattn_fwd_params {
     float scale;             /* logit scale (> 0), e.g. D^-1/2               */
     int32_t sqrt_softmax;    /* 1: O = sum sqrt(P) V (muS variant)           */
     float dropout_p;         /* must be 0                                    */
+    void *workspace;         /* >= mpattn_fwd_workspace_size() bytes, 16-byte
+                                aligned; contents need no initialisation   */
+    int64_t workspace_bytes;
 } mpattn_fwd_params;
 
 typedef struct mpattn_bwd_params {
@@ -110,6 +113,11 @@ typedef struct mpattn_bwd_params {
     float scale;
     int32_t sqrt_softmax;
 } mpattn_bwd_params;
+
+/* Workspace bytes mpattn_fwd needs (chain-id staging; RoPE-rotated K_self
+ * when rope == MPATTN_ROPE_FUSED). */
+int64_t mpattn_fwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D, int32_t dtype,
+                                  int32_t rope);
 
 /* Forward. Replaces fused_multi_pathway_attention
  * (mint_plus/models/kernels/multi_pathway_attention.py:184-279) and

@@ -60,6 +60,7 @@ class FwdParams(ctypes.Structure):
         ("dtype", ctypes.c_int32), ("rope", ctypes.c_int32),
         ("scale", ctypes.c_float), ("sqrt_softmax", ctypes.c_int32),
         ("dropout_p", ctypes.c_float),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -87,6 +88,7 @@ class BwdParams(ctypes.Structure):
 EXPORTS = {
     "mpattn_fwd": (ctypes.c_int, [ctypes.POINTER(FwdParams), ctypes.c_void_p]),
     "mpattn_bwd": (ctypes.c_int, [ctypes.POINTER(BwdParams), ctypes.c_void_p]),
+    "mpattn_fwd_workspace_size": (ctypes.c_int64, [ctypes.c_int32] * 6),
     "mpattn_bwd_workspace_size": (ctypes.c_int64, [ctypes.c_int32] * 4),
     "mpattn_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "mpattn_last_error": (ctypes.c_char_p, []),
@@ -262,9 +264,16 @@ def mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, *, chain_ids=N
     p.scale = float(scale)
     p.sqrt_softmax = 1 if sqrt_softmax else 0
     p.dropout_p = float(dropout_p)
-    rc = load_library().mpattn_fwd(ctypes.byref(p), _stream_handle(dev))
+    lib = load_library()
+    ws_bytes = lib.mpattn_fwd_workspace_size(B, H, L, D, p.dtype, p.rope)
+    if ws_bytes < 0:
+        raise MpattnError(MPATTN_ERR_INVALID, "mpattn_fwd_workspace_size", "bad shape")
+    # torch's caching allocator returns 512-byte aligned blocks
+    ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device=dev)
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
+    rc = lib.mpattn_fwd(ctypes.byref(p), _stream_handle(dev))
     _check(rc, "mpattn_fwd")
-    del keep, ins
+    del keep, ins, ws
     return (out, lse) if need_lse else out
 
 

@@ -12,6 +12,7 @@
 
 namespace mpattn {
 hipError_t launch_fwd16(const mpattn_fwd_params& p, hipStream_t stream);
+int64_t fwd_workspace_bytes(int B, int H, int L, int D, int dtype, int rope);
 hipError_t launch_fwd32(const mpattn_fwd_params& p, hipStream_t stream);
 hipError_t launch_bwd(const mpattn_bwd_params& p, hipStream_t stream);
 int64_t bwd_workspace_bytes(int B, int H, int L, int D);
@@ -108,6 +109,17 @@ int mpattn_fwd(const mpattn_fwd_params* p, void* stream) {
     for (int i = 0; i < 7; ++i)
         if ((rc = check_tensor(*ts[i], names[i], es, i == 6))) return rc;
     if (p->lse && (uintptr_t)p->lse % 4) return fail(MPATTN_ERR_INVALID, "lse misaligned");
+    // Rows are addressed with 32-bit byte offsets from each (b, h) base.
+    for (int i = 0; i < 6; ++i)
+        if ((int64_t)p->L * ts[i]->stride_t * es + 64 * es > 0x7fffffffLL)
+            return fail(MPATTN_ERR_UNSUPPORTED, "%s: L * stride_t too large for 32-bit row offsets",
+                        names[i]);
+    if (p->dtype != MPATTN_FP32) {
+        const int64_t need = mpattn::fwd_workspace_bytes(p->B, p->H, p->L, p->D, p->dtype, p->rope);
+        if (!p->workspace || (uintptr_t)p->workspace % 256 || p->workspace_bytes < need)
+            return fail(MPATTN_ERR_INVALID, "workspace: need %lld bytes, 256-byte aligned (got %lld)",
+                        (long long)need, (long long)p->workspace_bytes);
+    }
     hipError_t e;
     if (p->dtype == MPATTN_FP32) {
         e = mpattn::launch_fwd32(*p, (hipStream_t)stream);
@@ -117,6 +129,12 @@ int mpattn_fwd(const mpattn_fwd_params* p, void* stream) {
     }
     if (e != hipSuccess) return fail(MPATTN_ERR_LAUNCH, "fwd launch: %s", hipGetErrorString(e));
     return MPATTN_OK;
+}
+
+int64_t mpattn_fwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D, int32_t dtype,
+                                  int32_t rope) {
+    if (B < 1 || H < 1 || L < 1) return -1;
+    return mpattn::fwd_workspace_bytes(B, H, L, D, dtype, rope);
 }
 
 int64_t mpattn_bwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D) {

@@ -4,29 +4,40 @@
 // (mint_plus/models/modules_plus.py:155-201 with the fp32 softmax of
 // mint_plus/models/mu_scaling/layer.py:159) and the flash-style contract of
 // mint_plus/models/kernels/multi_pathway_attention.py:32-181, re-designed for
-// CDNA4:
+// CDNA4. Two launches:
 //
-// * A workgroup of W wavefronts owns 32*W consecutive queries of one (b, h);
-//   each wavefront owns 32 of them.
-// * Keys stream through LDS in stages of 64 (two 32-key subtiles). K rows are
-//   stored row-major, V is stored transposed (d-major) so that the PV operand
-//   is one 16-byte LDS read per lane. RoPE and the logit scale are applied in
-//   fp32 while Q is loaded and while K_self is staged.
-// * Per 32-key subtile a wavefront computes S^T = K Q^T with
-//   v_mfma_f32_32x32x16 (rows = keys, columns = queries). Lane l then holds 16
-//   logits of query l%32, so the softmax row max/sum are in-lane reductions
-//   plus one exchange with lane l^32. K rows are read in an order that swaps
-//   bits 2 and 3 of the row index, which makes accumulator slot i of lane half
-//   hh correspond to key 16*(i/8) + 8*hh + i%8: the probabilities are then
-//   already laid out as the B operand of O^T += V^T P^T, with no shuffle.
-// * Subtiles are classified from the chain-id range of their keys and of the
-//   wavefront's queries: pure same-chain subtiles run only the self pathway,
-//   pure cross-chain subtiles only the multimer pathway; mixed or padded
-//   subtiles compute both logits and select per element.
-// * Online softmax in base 2 with a lazily updated reference max: the
-//   accumulators are rescaled only when a row max grows by more than 2^8.
-// * For D < 32 the unused rows of the V^T operand hold ones, so the MFMA also
-//   produces the softmax denominator; otherwise it is summed in fp32.
+// 1. fwd_prep_kernel (memory-bound, small): effective chain id per key (the
+//    chain id, or kPadChain for padded keys and keys past L), a per-32-key
+//    summary (min/max chain id over valid keys, number of padded keys) and,
+//    with fused RoPE, K_self rotated once into the workspace.
+//
+// 2. fwd_kernel:
+//  * A workgroup of W wavefronts owns 32*W consecutive queries of one (b, h);
+//    each wavefront owns 32 of them. Q is loaded once, RoPE and the logit
+//    scale applied in fp32.
+//  * Keys stream through a ring of NBUF LDS stages of 64 keys. Each stage holds
+//    K_self, K_multi, V_self, V_multi tiles copied by global_load_lds (16 bytes
+//    per lane, straight into LDS, no register round trip), issued NBUF-1
+//    stages ahead of use, one barrier per stage. Rows are stored densely with
+//    their 16-byte chunks XOR-swizzled by row to spread LDS banks.
+//  * Per 32-key subtile a wavefront computes S^T = K Q^T with
+//    v_mfma_f32_32x32x16 (rows = keys, columns = queries): lane l holds 16
+//    logits of query l%32, so the softmax row statistics are in-lane. K rows
+//    are read with bits 2 and 3 of the row index swapped, which makes
+//    accumulator slot i of lane half hh the key 16*(i/8) + 8*hh + i%8: the
+//    probabilities are then already the B operand of O^T += V^T P^T. The V^T
+//    operand comes from the row-major V tile via ds_read_b64_tr_b16.
+//  * Stages are classified from the per-32-key chain summaries and the
+//    wavefront's query chain range: pure same-chain stages run only the self
+//    pathway, pure cross-chain stages only the multimer pathway (one softmax
+//    update over 64 keys); mixed or padded subtiles compute both logits and
+//    select per element.
+//  * Online softmax in base 2 with a lazily updated reference max: nothing is
+//    rescaled unless a row max grows by more than 2^8, and only then do the
+//    two lane halves of a query exchange their maxima.
+//  * Row sums come from v_dot2_f32_bf16 on the rounded probabilities (the
+//    values the PV MFMA consumes). For D < 32 the unused rows of the V^T
+//    operand are ones, so the MFMA produces the sum.
 #include <type_traits>
 
 #include "mpattn_common.h"
@@ -35,45 +46,212 @@ namespace mpattn {
 
 constexpr int kBN = 64;  // keys per LDS stage
 
+inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+// Workspace layout (offsets 256-byte aligned):
+//   keff int32 [B][Lp]          effective chain id per key
+//   ksum int32 [B][Lp/32][4]    min chain, max chain, #padded, 0
+//   krot T     [B][H][Lp][D]    RoPE-rotated K_self (fused RoPE only)
+struct FwdWs {
+    int64_t keff, ksum, krot, total;
+};
+
+inline FwdWs fwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
+    const int64_t Lp = round_up(L, kBN);
+    auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+    FwdWs w;
+    w.keff = 0;
+    w.ksum = al(w.keff + (int64_t)B * Lp * 4);
+    w.krot = al(w.ksum + (int64_t)B * (Lp / 32) * 16);
+    w.total = al(w.krot + (rope ? (int64_t)B * H * Lp * D * esize : 0));
+    return w;
+}
+
+int64_t fwd_workspace_bytes(int B, int H, int L, int D, int dtype, int rope) {
+    const int es = dtype == MPATTN_FP32 ? 4 : 2;
+    return fwd_ws_layout(B, H, L, D, es, rope == MPATTN_ROPE_FUSED).total;
+}
+
+struct FwdArgs {
+    mpattn_fwd_params p;
+    const int* keff;
+    const int* ksum;
+    const void* krot;
+    int Lp;
+    float qmul;    // factor applied to q while loading (scale when fused, else 1)
+    float c;       // base-2 factor applied to raw logits
+    float lse_mul; // raw logit -> natural-unit logit
+};
+
+// ---------------------------------------------------------------------------
+// Prep: chain staging (blocks [0, nchain)) and K_self rotation (the rest).
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool ROPE, bool DENSE>
+__global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p, int* keff,
+                                                       int* ksum, T* krot, int Lp, int nchain) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int L = p.L;
+    if ((int)blockIdx.x < nchain) {
+        const int ngrp = Lp / 64;
+        const int gid = blockIdx.x * 4 + wave;
+        if (gid >= p.B * ngrp) return;
+        const int b = gid / ngrp, k0 = (gid % ngrp) * 64;
+        const int kg = k0 + lane;
+        int cid = kPadChain;
+        if (kg < L && !(p.key_pad && p.key_pad[(int64_t)b * L + kg]))
+            cid = DENSE ? 0 : p.chain_id[(int64_t)b * L + kg];
+        keff[(int64_t)b * Lp + kg] = cid;
+        const bool valid = cid != kPadChain;
+        const int mn = half_min_i(valid ? cid : INT32_MAX);
+        const int mx = half_max_i(valid ? cid : INT32_MIN);
+        const uint64_t padm = __ballot(!valid);
+        if ((lane & 31) == 0) {
+            const int hh = lane >> 5;
+            int* o = ksum + ((int64_t)b * (Lp / 32) + (k0 >> 5) + hh) * 4;
+            o[0] = mn;
+            o[1] = mx;
+            o[2] = __popcll(hh ? (padm >> 32) : (padm & 0xffffffffull));
+            o[3] = 0;
+        }
+        return;
+    }
+    if constexpr (ROPE) {
+        typedef typename Elt<T>::v8 v8;
+        constexpr int H2 = D / 2;
+        constexpr int NPC = (H2 % 8 == 0) ? H2 / 8 : 1;  // work items per row
+        const int64_t item = (int64_t)(blockIdx.x - nchain) * 256 + tid;
+        const int64_t rows = (int64_t)p.B * p.H * Lp;
+        if (item >= rows * NPC) return;
+        const int64_t row = item / NPC;
+        const int pc = (int)(item % NPC);
+        const int t = (int)(row % Lp);
+        const int bh = (int)(row / Lp);
+        const int b = bh / p.H, h = bh % p.H;
+        T* dst = krot + row * D;
+        const T* src = (const T*)p.k_self.ptr + b * p.k_self.stride_b + h * p.k_self.stride_h +
+                       (int64_t)t * p.k_self.stride_t;
+        if constexpr (H2 % 8 == 0) {
+            const int d0 = pc * 8;
+            float lo[8], hi[8];
+            if (t < L) {
+                float x[8], y[8];
+                load8f<T>(src, d0, x);
+                load8f<T>(src, d0 + H2, y);
+                const float* cr = p.rope_cos + (int64_t)t * H2 + d0;
+                const float* sr = p.rope_sin + (int64_t)t * H2 + d0;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    lo[u] = x[u] * cr[u] - y[u] * sr[u];
+                    hi[u] = y[u] * cr[u] + x[u] * sr[u];
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) lo[u] = hi[u] = 0.f;
+            }
+            *reinterpret_cast<v8*>(dst + d0) = pack8<T>(lo);
+            *reinterpret_cast<v8*>(dst + d0 + H2) = pack8<T>(hi);
+        } else {
+            // D = 24: one thread per row.
+#pragma unroll
+            for (int d0 = 0; d0 < D; d0 += 8) {
+                float x[8];
+                if (t < L) load8_rot<T, D>(src, p.rope_cos, p.rope_sin, t, d0, 1.0f, true, x);
+                else
+                    for (int u = 0; u < 8; ++u) x[u] = 0.f;
+                *reinterpret_cast<v8*>(dst + d0) = pack8<T>(x);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Main kernel.
+// ---------------------------------------------------------------------------
 template <int D> struct FwdShape {
     static constexpr int DP = D <= 16 ? 16 : (D <= 32 ? 32 : 64);  // MFMA K for QK^T
     static constexpr int NKK = DP / 16;                              // QK MFMAs / subtile
     static constexpr int NDB = DP <= 32 ? 1 : 2;                     // 32-row blocks of O^T
-    static constexpr int VROWS = NDB * 32;
     static constexpr bool SUM_MFMA = D < 32;                         // ones rows give the sum
     static constexpr int ISUM = 4 * (D / 8);                         // accumulator slot of row D
-    static constexpr int KST = DP + 8;                               // LDS row stride, K
-    static constexpr int VST = kBN + 8;                              // LDS row stride, V^T
+    static constexpr int RB = D * 2;                                 // LDS row bytes
+    static constexpr int NCH = RB / 16;                              // 16-byte chunks per row
+    static constexpr int TILE = kBN * RB;                            // bytes per tensor tile
+    static constexpr int STAGE = 4 * TILE;
+    static constexpr int NI = TILE / 1024;                           // DMA wave-instr per tile
+    static constexpr bool POW2 = (NCH & (NCH - 1)) == 0;
+    static constexpr int ROWS_PER_256 = 256 / RB;
+    // physical 16-byte chunk of logical chunk c in row r
+    static __device__ __forceinline__ int swz(int r, int c) {
+        if constexpr (POW2) return c ^ ((r / ROWS_PER_256) & (NCH - 1));
+        return c;
+    }
 };
 
-struct FwdArgs {
-    mpattn_fwd_params p;
-    float qmul;   // factor applied to q while loading (scale when fused, else 1)
-    float c;      // base-2 factor applied to raw logits
-    float lse_mul;// raw logit -> natural-unit logit
-};
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ unsigned lds_addr(const void* ptr) {
+    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
+}
 
-// Query-side state carried by one wavefront.
-template <typename T, int D> struct QFrag {
-    typename Elt<T>::v8 f[2][FwdShape<D>::NKK];  // [pathway][k-chunk]
-};
+// global -> LDS copy (global_load_lds): lane i writes its `size` bytes at LDS
+// address lds + i*size; the global address is sbase + voff (per lane).
+// Issued as inline asm so the compiler does not wait for it before unrelated
+// LDS reads; completion is tracked by hand with wait_vm<> and the barrier.
+// M0 (the LDS base register) is saved and restored around the copy.
+__device__ __forceinline__ void dma16(const void* sbase, unsigned voff, unsigned lds) {
+    int tmp;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(tmp) : "v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* sbase, unsigned voff, unsigned lds) {
+    int tmp;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+        "global_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(tmp) : "v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
 
-template <typename T, int D, int W, bool ROPE, bool DENSE>
+// Wait until at most N vector-memory instructions of this wave are in flight.
+template <int N> __device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Scalar (wave-uniform) 16-byte load: keeps the vector-memory counter free
+// for the LDS copies in flight.
+__device__ __forceinline__ int4 sload4(const int4* ptr) {
+    int4 r;
+    asm volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(r) : "s"(ptr) : "memory");
+    return r;
+}
+
+// Workgroup barrier without the release fence of __syncthreads (which would
+// also drain the stages still in flight); LDS reads of this wave complete first.
+__device__ __forceinline__ void stage_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <typename T, int D, int W, int NBUF, bool ROPE, bool DENSE>
 __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
     using S = FwdShape<D>;
     using E = Elt<T>;
     typedef typename E::v8 v8;
+    typedef typename E::v2 v2;
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    typedef short s8 __attribute__((ext_vector_type(8)));
+    constexpr int TOT = 4 * S::NI;  // DMA instructions per stage
+    static_assert(TOT % W == 0, "stage DMA must split evenly over waves");
+    constexpr int IPW = TOT / W + 1;  // per wave per stage, incl. the chain ids
     const mpattn_fwd_params& p = args.p;
 
-    __shared__ __attribute__((aligned(16))) T sK[2][kBN * S::KST];
-    __shared__ __attribute__((aligned(16))) T sVt[2][S::VROWS * S::VST];
-    __shared__ __attribute__((aligned(16))) int sCid[kBN];
-    __shared__ int sSum[2][4];
+    __shared__ __attribute__((aligned(1024))) char smem[NBUF * S::STAGE];
+    __shared__ __attribute__((aligned(16))) int scid[W][NBUF][kBN];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
-    const int L = p.L, H = p.H;
+    const int L = p.L, H = p.H, Lp = args.Lp;
     const int nqb = (L + 32 * W - 1) / (32 * W);
     const int g = xcd_remap(blockIdx.x, gridDim.x);
     const int qb = g % nqb, bh = g / nqb;
@@ -81,28 +259,64 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
     const int q = qb * 32 * W + wave * 32 + ql;
     const bool qvalid = q < L;
 
-    // (b, h) base of each operand; pathway 0 = self, 1 = multimer.
     auto base = [&](const mpattn_tensor& t) {
         return (const T*)t.ptr + b * t.stride_b + h * t.stride_h;
     };
     const T* const qs_p = base(p.q_self);
     const T* const qm_p = base(p.q_multi);
-    const T* const ks_p = base(p.k_self);
     const T* const km_p = base(p.k_multi);
     const T* const vs_p = base(p.v_self);
     const T* const vm_p = base(p.v_multi);
+    const T* const ks_p = ROPE ? (const T*)args.krot + (int64_t)bh * Lp * D : base(p.k_self);
+    const int64_t ks_t = ROPE ? D : p.k_self.stride_t;
+    const int64_t km_t = p.k_multi.stride_t, vs_t = p.v_self.stride_t, vm_t = p.v_multi.stride_t;
+    const int* const keff_b = args.keff + (int64_t)b * Lp;
+    const int4* const ksum_b = reinterpret_cast<const int4*>(args.ksum) + (int64_t)b * (Lp / 32);
 
-    // Ones rows of V^T (rows D..VROWS-1) turn the PV MFMA into a row-sum too.
-    if constexpr (S::SUM_MFMA) {
-        for (int i = tid; i < 2 * (S::VROWS - D) * kBN; i += W * 64) {
-            const int pw = i / ((S::VROWS - D) * kBN);
-            const int r = i % ((S::VROWS - D) * kBN);
-            sVt[pw][(D + r / kBN) * S::VST + r % kBN] = (T)1.0f;
-        }
+    // ---- DMA plan: this wave's TOT/W tile copies per stage ----
+    // Copy j covers 16-byte slots [64*part, 64*part + 64) of tensor `ten`;
+    // lane -> (row r, logical chunk c) with the physical slot swizzled.
+    constexpr int NJ = TOT / W;
+    const char* dsb[NJ];     // (b, h) base of the source tensor (uniform)
+    unsigned dstr[NJ];       // row stride in bytes (uniform)
+    unsigned dlds[NJ];       // LDS offset inside a stage (uniform)
+    unsigned dloff[NJ];      // per-lane byte offset of (r, c) relative to row 0
+    int drow[NJ], dcol[NJ];  // per-lane row and chunk byte offset
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int ins = wave + j * W;
+        const int ten = ins / S::NI, part = ins % S::NI;
+        const int slot = part * 64 + lane;
+        const int r = slot / S::NCH, pc = slot % S::NCH;
+        const int cb = S::swz(r, pc) * 16;  // swz is an involution on the chunk index
+        const T* tb = ten == 0 ? ks_p : ten == 1 ? km_p : ten == 2 ? vs_p : vm_p;
+        const int64_t ts = ten == 0 ? ks_t : ten == 1 ? km_t : ten == 2 ? vs_t : vm_t;
+        dsb[j] = (const char*)tb;
+        dstr[j] = (unsigned)(ts * (int64_t)sizeof(T));
+        dlds[j] = ten * S::TILE + part * 1024;
+        drow[j] = r;
+        dcol[j] = cb;
+        dloff[j] = r * dstr[j] + cb;
     }
+    const unsigned smem_base = lds_addr(smem);
+    const unsigned scid_base = lds_addr(&scid[wave][0][0]);
+
+    // ---- issue the DMA of stage s into buffer bf ----
+    auto issue = [&](int s, int bf) {
+        const int k0 = s * kBN;
+        const bool tail = k0 + kBN > L;  // uniform: clamp rows past L to L-1
+        const unsigned lb = smem_base + bf * S::STAGE;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            unsigned voff = (unsigned)k0 * dstr[j] + dloff[j];
+            if (tail) voff = (unsigned)min(k0 + drow[j], L - 1) * dstr[j] + dcol[j];
+            dma16(dsb[j], voff, lb + dlds[j]);
+        }
+        dma4(keff_b, (unsigned)(k0 + lane) * 4u, scid_base + bf * kBN * 4);
+    };
 
     // ---- Q fragments (B operand of S^T = K Q^T): dims kk*16 + 8*hh + [0,8) ----
-    QFrag<T, D> qf;
+    v8 qf[2][S::NKK];
 #pragma unroll
     for (int pw = 0; pw < 2; ++pw) {
 #pragma unroll
@@ -111,16 +325,15 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
             if (qvalid) {
                 const T* row = pw == 0 ? qs_p + (int64_t)q * p.q_self.stride_t
                                        : qm_p + (int64_t)q * p.q_multi.stride_t;
-                load8_rot<T, D>(row, p.rope_cos, p.rope_sin, q,
-                                kk * 16 + hh * 8, args.qmul, ROPE && pw == 0, x);
+                load8_rot<T, D>(row, p.rope_cos, p.rope_sin, q, kk * 16 + hh * 8, args.qmul,
+                                ROPE && pw == 0, x);
             } else {
 #pragma unroll
                 for (int t = 0; t < 8; ++t) x[t] = 0.f;
             }
-            qf.f[pw][kk] = pack8<T>(x);
+            qf[pw][kk] = pack8<T>(x);
         }
     }
-
     int cq = 0, cq_min = 0, cq_max = 0;
     if constexpr (!DENSE) {
         cq = qvalid ? p.chain_id[(int64_t)b * L + q] : 0;
@@ -132,6 +345,7 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
         mrow = p.chain_mask + (int64_t)b * p.mask_stride_b + (int64_t)(qvalid ? q : 0) * p.mask_stride_q;
     }
 
+    // ---- online softmax state ----
     const float c = args.c;
     const float th = 8.0f / c;  // rescale threshold in raw logit units (2^8)
     float m_ref = -INFINITY;
@@ -142,204 +356,215 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
 
-    // Row of the K operand this lane reads: subtile row ql with bits 2,3 swapped.
+    // K operand row: subtile row ql with bits 2,3 swapped.
     const int krow = (ql & ~12) | ((ql & 4) << 1) | ((ql & 8) >> 1);
-
-    for (int k0 = 0; k0 < L; k0 += kBN) {
-        __syncthreads();  // previous stage fully consumed
-        // ---- stage K (row-major, RoPE on self) ----
-        constexpr int KCH = S::DP / 8;  // 8-element chunks per row
-        for (int it = tid; it < 2 * kBN * KCH; it += W * 64) {
-            const int pw = it / (kBN * KCH);
-            const int r = (it / KCH) % kBN;
-            const int d0 = (it % KCH) * 8;
-            const int kg = k0 + r;
-            float x[8];
-            if (kg < L) {
-                const T* row = pw == 0 ? ks_p + (int64_t)kg * p.k_self.stride_t
-                                       : km_p + (int64_t)kg * p.k_multi.stride_t;
-                load8_rot<T, D>(row, p.rope_cos, p.rope_sin, kg, d0, 1.0f, ROPE && pw == 0, x);
-            } else {
+    v8 zero8, one8;
 #pragma unroll
-                for (int t = 0; t < 8; ++t) x[t] = 0.f;
-            }
-            *reinterpret_cast<v8*>(&sK[pw][r * S::KST + d0]) = pack8<T>(x);
+    for (int t = 0; t < 8; ++t) { zero8[t] = (T)0.f; one8[t] = (T)1.0f; }
+
+    // A operand of S^T = K Q^T: K rows, dims kk*16 + 8*hh + [0, 8).
+    auto kop = [&](const char* stage, int ten, int st, int kk) -> v8 {
+        const int cch = 2 * kk + hh;
+        if (cch >= S::NCH) return zero8;  // D = 24: dims [24, 32)
+        const int r = st * 32 + krow;
+        return *reinterpret_cast<const v8*>(stage + ten * S::TILE + r * S::RB + S::swz(r, cch) * 16);
+    };
+    // A operand of O^T += V^T P^T for d block db: V[key(slot j)][d = db*32 + l%32]
+    // via two ds_read_b64_tr_b16 (each: 4 keys x 4 dims per 16-lane group).
+    const int tg = lane >> 4, ti = lane & 15;
+    auto vop = [&](const char* stage, int ten, int st, int cc, int db) -> v8 {
+        const int d = db * 32 + (lane & 31);
+        int e = 8 * db + 4 * (tg & 1) + (ti & 3);  // 8-byte chunk this lane addresses
+        if (8 * e >= S::RB) e = ti & 3;          // keep addresses in bounds (result unused)
+        s4 half[2];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int row = st * 32 + 16 * cc + 8 * (tg >> 1) + 4 * rr + (ti >> 2);
+            const char* ptr = stage + ten * S::TILE + row * S::RB + S::swz(row, e >> 1) * 16 + (e & 1) * 8;
+            half[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(ptr));
         }
-        // ---- stage V^T (d-major); each item: 2 keys x 8 dims ----
-        constexpr int VCH = D / 8;
-        for (int it = tid; it < 2 * (kBN / 2) * VCH; it += W * 64) {
-            const int pw = it / ((kBN / 2) * VCH);
-            const int kp2 = (it / VCH) % (kBN / 2);
-            const int d0 = (it % VCH) * 8;
-            const int kg = k0 + 2 * kp2;
-            const T* vb = pw == 0 ? vs_p : vm_p;
-            const int64_t vstr = pw == 0 ? p.v_self.stride_t : p.v_multi.stride_t;
-            float x0[8], x1[8];
-            if (kg < L) load8f<T>(vb + (int64_t)kg * vstr, d0, x0);
-            else for (int t = 0; t < 8; ++t) x0[t] = 0.f;
-            if (kg + 1 < L) load8f<T>(vb + (int64_t)(kg + 1) * vstr, d0, x1);
-            else for (int t = 0; t < 8; ++t) x1[t] = 0.f;
+        // Whole-vector bitcast: element-wise i16 -> bf16 inserts are mis-lowered.
+        const v8 r8 = __builtin_bit_cast(v8, __builtin_shufflevector(half[0], half[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        if constexpr (D % 32 == 0) return r8;
+        return d < D ? r8 : one8;
+    };
+
+    auto update_max = [&](float mx) {
+        if (__any(mx > m_ref + th)) {
+            const float mxa = fmaxf(mx, __shfl_xor(mx, 32));
+            const bool upd = mxa > m_ref + th;
+            const float m_new = upd ? mxa : m_ref;
+            const float alpha = upd ? fast_exp2((m_ref - m_new) * c) : 1.0f;
+            m_ref = m_new;
+            l_run *= alpha;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                typename Elt<T>::v2 pr2;
-                pr2[0] = (T)x0[t];
-                pr2[1] = (T)x1[t];
-                *reinterpret_cast<typename Elt<T>::v2*>(&sVt[pw][(d0 + t) * S::VST + 2 * kp2]) = pr2;
-            }
+            for (int db = 0; db < S::NDB; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
         }
-        // ---- chain ids / padding, and per-subtile summary (wave 0) ----
-        if (wave == 0) {
-            const int kg = k0 + lane;
-            int cid = kPadChain;
-            if (kg < L && !(p.key_pad && p.key_pad[(int64_t)b * L + kg])) {
-                cid = DENSE ? 0 : p.chain_id[(int64_t)b * L + kg];
-            }
-            sCid[lane] = cid;
-            const bool valid = cid != kPadChain;
-            const int mn = half_min_i(valid ? cid : INT32_MAX);
-            const int mx = half_max_i(valid ? cid : INT32_MIN);
-            const uint64_t padm = __ballot(!valid);
-            if ((lane & 31) == 0) {
-                sSum[hh][0] = mn;
-                sSum[hh][1] = mx;
-                sSum[hh][2] = __popcll(hh ? (padm >> 32) : (padm & 0xffffffffull));
-            }
+    };
+
+    // One pathway over NS consecutive subtiles starting at subtile st0.
+    auto pure = [&](auto pw_c, auto ns_c, const char* stage, int st0) {
+        constexpr int pw = decltype(pw_c)::value;
+        constexpr int NS = decltype(ns_c)::value;
+        // All LDS operands of the step are read up front: the V reads then
+        // overlap the softmax.
+        v8 ka[NS][S::NKK], va[NS][2][S::NDB];
+#pragma unroll
+        for (int st = 0; st < NS; ++st)
+#pragma unroll
+            for (int kk = 0; kk < S::NKK; ++kk) ka[st][kk] = kop(stage, pw, st0 + st, kk);
+#pragma unroll
+        for (int st = 0; st < NS; ++st)
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+                for (int db = 0; db < S::NDB; ++db) va[st][cc][db] = vop(stage, 2 + pw, st0 + st, cc, db);
+        f32x16 sv[NS];
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sv[st][i] = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < S::NKK; ++kk) sv[st] = E::mma(ka[st][kk], qf[pw][kk], sv[st]);
         }
-        __syncthreads();
-
+        float mx = sv[0][0];
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            const int kmin = __builtin_amdgcn_readfirstlane(sSum[st][0]);
-            const int kmax = __builtin_amdgcn_readfirstlane(sSum[st][1]);
-            const int npad = __builtin_amdgcn_readfirstlane(sSum[st][2]);
-            if (npad == 32) continue;
-            int mode = 2;  // 0: pure self, 1: pure multimer, 2: general
-            if (!DENSE && npad == 0) {
-                if (kmin == kmax && cq_min == cq_max && kmin == cq_min) mode = 0;
-                else if (kmax < cq_min || kmin > cq_max) mode = 1;
-            }
-            const int kbase = st * 32;
-            const int krd = (kbase + krow) * S::KST + hh * 8;  // K operand offset
-
-            // Online softmax (base 2, lazy rescale): updates m_ref / l_run / o
-            // for this subtile's logits and returns the unnormalised weights.
-            auto softmax_step = [&](const f32x16& sv, float pr[16]) {
-                float mx = sv[0];
+        for (int st = 0; st < NS; ++st)
 #pragma unroll
-                for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
-                const bool need = mx > m_ref + th;
-                if (__any(need)) {
-                    const float m_new = need ? mx : m_ref;
-                    const float alpha = need ? fast_exp2((m_ref - m_new) * c) : 1.0f;
-                    m_ref = m_new;
-                    l_run *= alpha;
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sv[st][i]);
+        update_max(mx);
+        const float mc = m_ref * c;
 #pragma unroll
-                    for (int db = 0; db < S::NDB; ++db)
+        for (int st = 0; st < NS; ++st) {
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-                }
-                const float mc = m_ref * c;
+            for (int cc = 0; cc < 2; ++cc) {
+                float pr[8];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) pr[i] = fast_exp2(fmaf(sv[i], c, -mc));
-            };
-
-            // One pathway for the whole subtile.
-            auto pure = [&](auto pw_c) {
-                constexpr int pw = decltype(pw_c)::value;
-                f32x16 sv;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) sv[i] = 0.f;
-#pragma unroll
-                for (int kk = 0; kk < S::NKK; ++kk) {
-                    const v8 a = *reinterpret_cast<const v8*>(&sK[pw][krd + kk * 16]);
-                    sv = E::mma(a, qf.f[pw][kk], sv);
-                }
-                float pr[16];
-                softmax_step(sv, pr);
-                v8 pb[2];
-#pragma unroll
-                for (int cc = 0; cc < 2; ++cc) pb[cc] = pack8<T>(&pr[8 * cc]);
+                for (int t = 0; t < 8; ++t) pr[t] = fast_exp2(fmaf(sv[st][8 * cc + t], c, -mc));
+                const v8 pb = pack8<T>(pr);
                 if constexpr (!S::SUM_MFMA) {
 #pragma unroll
-                    for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-                        for (int t = 0; t < 8; ++t) l_run += (float)pb[cc][t];
+                    for (int t = 0; t < 8; t += 2) l_run = E::sum2(v2{pb[t], pb[t + 1]}, l_run);
                 }
 #pragma unroll
-                for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-                    for (int db = 0; db < S::NDB; ++db) {
-                        const v8 a = *reinterpret_cast<const v8*>(
-                            &sVt[pw][(db * 32 + ql) * S::VST + kbase + 16 * cc + 8 * hh]);
-                        o[db] = E::mma(a, pb[cc], o[db]);
-                    }
-            };
+                for (int db = 0; db < S::NDB; ++db) o[db] = E::mma(va[st][cc][db], pb, o[db]);
+            }
+        }
+    };
 
-            // Both pathways, selected per element; handles padded keys.
-            auto general = [&]() {
-                f32x16 ss, sm, sv;
+    // Both pathways on one subtile, selected per element; handles padded keys.
+    auto general = [&](const char* stage, const int* cid, int st, int k0) {
+        f32x16 ss, sm, sv;
 #pragma unroll
-                for (int i = 0; i < 16; ++i) { ss[i] = 0.f; sm[i] = 0.f; }
+        for (int i = 0; i < 16; ++i) { ss[i] = 0.f; sm[i] = 0.f; }
 #pragma unroll
-                for (int kk = 0; kk < S::NKK; ++kk) {
-                    const v8 as = *reinterpret_cast<const v8*>(&sK[0][krd + kk * 16]);
-                    const v8 am = *reinterpret_cast<const v8*>(&sK[1][krd + kk * 16]);
-                    ss = E::mma(as, qf.f[0][kk], ss);
-                    sm = E::mma(am, qf.f[1][kk], sm);
+        for (int kk = 0; kk < S::NKK; ++kk) {
+            ss = E::mma(kop(stage, 0, st, kk), qf[0][kk], ss);
+            sm = E::mma(kop(stage, 1, st, kk), qf[1][kk], sm);
+        }
+        bool same[16];
+        // keys of slot i: st*32 + 16*(i/8) + 8*hh + i%8
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const int kl = st * 32 + 16 * cc + 8 * hh;
+            const i32x4 c0 = *reinterpret_cast<const i32x4*>(&cid[kl]);
+            const i32x4 c1 = *reinterpret_cast<const i32x4*>(&cid[kl + 4]);
+            uint32_t mbits = 0;
+            if constexpr (DENSE) {
+                const int kg = k0 + kl;
+                for (int t = 0; t < 8; ++t)
+                    if (kg + t < L)
+                        mbits |= (uint32_t)(mrow[(int64_t)(kg + t) * p.mask_stride_k] != 0) << t;
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int ck = t < 4 ? c0[t & 3] : c1[t & 3];
+                const int i = 8 * cc + t;
+                const bool sm_ = DENSE ? !((mbits >> t) & 1u) : (ck == cq);
+                same[i] = sm_;
+                const float v = sm_ ? ss[i] : sm[i];
+                sv[i] = ck == kPadChain ? -INFINITY : v;
+            }
+        }
+        float mx = sv[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
+        update_max(mx);
+        const float mc = m_ref * c;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            v8 ps, pm;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int i = 8 * cc + t;
+                const T pv = (T)fast_exp2(fmaf(sv[i], c, -mc));
+                ps[t] = same[i] ? pv : (T)0.f;
+                pm[t] = same[i] ? (T)0.f : pv;
+            }
+            if constexpr (!S::SUM_MFMA) {
+#pragma unroll
+                for (int t = 0; t < 8; t += 2) {
+                    l_run = E::sum2(v2{ps[t], ps[t + 1]}, l_run);
+                    l_run = E::sum2(v2{pm[t], pm[t + 1]}, l_run);
                 }
-                bool same[16];
-                // keys of slot i: kbase + 16*(i/8) + 8*hh + i%8
+            }
 #pragma unroll
-                for (int cc = 0; cc < 2; ++cc) {
-                    const int kl = kbase + 16 * cc + 8 * hh;
-                    const i32x4 c0 = *reinterpret_cast<const i32x4*>(&sCid[kl]);
-                    const i32x4 c1 = *reinterpret_cast<const i32x4*>(&sCid[kl + 4]);
-                    uint32_t mbits = 0;
-                    if constexpr (DENSE) {
-                        const int kg = k0 + kl;
-                        for (int t = 0; t < 8; ++t)
-                            if (kg + t < L)
-                                mbits |= (uint32_t)(mrow[(int64_t)(kg + t) * p.mask_stride_k] != 0) << t;
-                    }
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        const int ck = t < 4 ? c0[t & 3] : c1[t & 3];
-                        const int i = 8 * cc + t;
-                        const bool sm_ = DENSE ? !((mbits >> t) & 1u) : (ck == cq);
-                        same[i] = sm_;
-                        const float v = sm_ ? ss[i] : sm[i];
-                        sv[i] = ck == kPadChain ? -INFINITY : v;
-                    }
-                }
-                float pr[16];
-                softmax_step(sv, pr);
-                v8 ps[2], pm[2];
-#pragma unroll
-                for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        const int i = 8 * cc + t;
-                        const T pv = (T)pr[i];
-                        if constexpr (!S::SUM_MFMA) l_run += (float)pv;
-                        ps[cc][t] = same[i] ? pv : (T)0.f;
-                        pm[cc][t] = same[i] ? (T)0.f : pv;
-                    }
-#pragma unroll
-                for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-                    for (int db = 0; db < S::NDB; ++db) {
-                        const int off = (db * 32 + ql) * S::VST + kbase + 16 * cc + 8 * hh;
-                        const v8 a0 = *reinterpret_cast<const v8*>(&sVt[0][off]);
-                        const v8 a1 = *reinterpret_cast<const v8*>(&sVt[1][off]);
-                        o[db] = E::mma(a0, ps[cc], o[db]);
-                        o[db] = E::mma(a1, pm[cc], o[db]);
-                    }
-            };
+            for (int db = 0; db < S::NDB; ++db) {
+                o[db] = E::mma(vop(stage, 2, st, cc, db), ps, o[db]);
+                o[db] = E::mma(vop(stage, 3, st, cc, db), pm, o[db]);
+            }
+        }
+    };
 
-            if (mode == 0) pure(std::integral_constant<int, 0>{});
-            else if (mode == 1) pure(std::integral_constant<int, 1>{});
-            else general();
+    auto subtile_mode = [&](int kmin, int kmax, int npad) {
+        // 0: pure self, 1: pure multimer, 2: general, 3: skip (all padded)
+        if (npad == 32) return 3;
+        if (!DENSE && npad == 0) {
+            if (kmin == kmax && cq_min == cq_max && kmin == cq_min) return 0;
+            if (kmax < cq_min || kmin > cq_max) return 1;
+        }
+        return 2;
+    };
+
+    // ---- main loop over stages ----
+    const int nst = (L + kBN - 1) / kBN;
+#pragma unroll
+    for (int t = 0; t < NBUF - 1; ++t)
+        if (t < nst) issue(t, t);
+    for (int s = 0; s < nst; ++s) {
+        const int bf = s % NBUF;
+        if constexpr (NBUF == 3) {
+            if (s + 1 < nst) wait_vm<IPW>();
+            else wait_vm<0>();
+        } else {
+            wait_vm<0>();
+        }
+        stage_barrier();
+        if (s + NBUF - 1 < nst) issue(s + NBUF - 1, (s + NBUF - 1) % NBUF);
+
+        const int4 sa = sload4(ksum_b + 2 * s);
+        const int4 sb = sload4(ksum_b + 2 * s + 1);
+        const int m0 = subtile_mode(sa.x, sa.y, sa.z);
+        const int m1 = subtile_mode(sb.x, sb.y, sb.z);
+        const char* stage = smem + bf * S::STAGE;
+        const int* cid = &scid[wave][bf][0];
+        const int k0 = s * kBN;
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        if (m0 == 0 && m1 == 0) {
+            pure(I0{}, I2{}, stage, 0);
+        } else if (m0 == 1 && m1 == 1) {
+            pure(I1{}, I2{}, stage, 0);
+        } else {
+            if (m0 == 0) pure(I0{}, I1{}, stage, 0);
+            else if (m0 == 1) pure(I1{}, I1{}, stage, 0);
+            else if (m0 == 2) general(stage, cid, 0, k0);
+            if (m1 == 0) pure(I0{}, I1{}, stage, 1);
+            else if (m1 == 1) pure(I1{}, I1{}, stage, 1);
+            else if (m1 == 2) general(stage, cid, 1, k0);
         }
     }
 
@@ -373,17 +598,36 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
 }
 
 template <typename T, int D, bool ROPE, bool DENSE>
-static hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
+static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     constexpr int W = 4;
-    const int nqb = (a.p.L + 32 * W - 1) / (32 * W);
-    const int64_t grid = (int64_t)a.p.B * a.p.H * nqb;
-    hipLaunchKernelGGL((fwd_kernel<T, D, W, ROPE, DENSE>), dim3((unsigned)grid), dim3(W * 64), 0,
+    constexpr int NBUF = D <= 32 ? 3 : 2;
+    const mpattn_fwd_params& p = a.p;
+    const int Lp = round_up(p.L, kBN);
+    a.Lp = Lp;
+    const FwdWs ws = fwd_ws_layout(p.B, p.H, p.L, D, sizeof(T), ROPE);
+    char* wsb = (char*)p.workspace;
+    int* keff = (int*)(wsb + ws.keff);
+    int* ksum = (int*)(wsb + ws.ksum);
+    T* krot = (T*)(wsb + ws.krot);
+    a.keff = keff;
+    a.ksum = ksum;
+    a.krot = krot;
+    const int nchain = (p.B * (Lp / 64) + 3) / 4;
+    constexpr int NPC = ((D / 2) % 8 == 0) ? D / 16 : 1;
+    const int64_t nrot = ROPE ? ((int64_t)p.B * p.H * Lp * NPC + 255) / 256 : 0;
+    hipLaunchKernelGGL((fwd_prep_kernel<T, D, ROPE, DENSE>), dim3((unsigned)(nchain + nrot)), dim3(256), 0,
+                       stream, p, keff, ksum, krot, Lp, nchain);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int nqb = (p.L + 32 * W - 1) / (32 * W);
+    const int64_t grid = (int64_t)p.B * p.H * nqb;
+    hipLaunchKernelGGL((fwd_kernel<T, D, W, NBUF, ROPE, DENSE>), dim3((unsigned)grid), dim3(W * 64), 0,
                        stream, a);
     return hipGetLastError();
 }
 
 template <typename T, int D>
-static hipError_t dispatch_fwd_d(const FwdArgs& a, hipStream_t s) {
+static hipError_t dispatch_fwd_d(FwdArgs& a, hipStream_t s) {
     const bool rope = a.p.rope == MPATTN_ROPE_FUSED;
     const bool dense = a.p.chain_mask != nullptr;
     if (rope) return dense ? launch_fwd<T, D, true, true>(a, s) : launch_fwd<T, D, true, false>(a, s);
@@ -391,7 +635,7 @@ static hipError_t dispatch_fwd_d(const FwdArgs& a, hipStream_t s) {
 }
 
 template <typename T>
-static hipError_t dispatch_fwd_t(const FwdArgs& a, hipStream_t s) {
+static hipError_t dispatch_fwd_t(FwdArgs& a, hipStream_t s) {
     switch (a.p.D) {
         case 16: return dispatch_fwd_d<T, 16>(a, s);
         case 24: return dispatch_fwd_d<T, 24>(a, s);
