@@ -78,9 +78,8 @@ struct FwdArgs {
     const int* ksum;
     const void* krot;
     int Lp;
-    float qmul;    // factor applied to q while loading (scale when fused, else 1)
-    float c;       // base-2 factor applied to raw logits
-    float lse_mul; // raw logit -> natural-unit logit
+    float qmul;    // factor applied to q while loading (scale*log2e when fused, else 1)
+    float c;       // base-2 factor applied to raw logits (1 when fused)
 };
 
 // ---------------------------------------------------------------------------
@@ -193,37 +192,29 @@ __device__ __forceinline__ unsigned lds_addr(const void* ptr) {
 }
 
 // global -> LDS copy (global_load_lds): lane i writes its `size` bytes at LDS
-// address lds + i*size; the global address is sbase + voff (per lane).
-// Issued as inline asm so the compiler does not wait for it before unrelated
-// LDS reads; completion is tracked by hand with wait_vm<> and the barrier.
-// M0 (the LDS base register) is saved and restored around the copy.
+// address M0 + i*size; the global address is sbase + voff (per lane). Issued
+// as inline asm so the compiler does not wait for it before unrelated LDS
+// reads; completion is tracked by hand with wait_vm<> and the barrier. M0 is
+// saved before a batch of copies and restored after it (m0_save/m0_restore).
+__device__ __forceinline__ int m0_save() {
+    int v;
+    asm volatile("s_mov_b32 %0, m0" : "=s"(v));
+    return v;
+}
+__device__ __forceinline__ void m0_restore(int v) { asm volatile("s_mov_b32 m0, %0" ::"s"(v)); }
 __device__ __forceinline__ void dma16(const void* sbase, unsigned voff, unsigned lds) {
-    int tmp;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
-        : "=&s"(tmp) : "v"(voff), "s"(sbase), "s"(lds) : "memory");
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :: "v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4(const void* sbase, unsigned voff, unsigned lds) {
-    int tmp;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
-        "global_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
-        : "=&s"(tmp) : "v"(voff), "s"(sbase), "s"(lds) : "memory");
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+                 :: "v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 
 // Wait until at most N vector-memory instructions of this wave are in flight.
 template <int N> __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Scalar (wave-uniform) 16-byte load: keeps the vector-memory counter free
-// for the LDS copies in flight.
-__device__ __forceinline__ int4 sload4(const int4* ptr) {
-    int4 r;
-    asm volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(r) : "s"(ptr) : "memory");
-    return r;
 }
 
 // Workgroup barrier without the release fence of __syncthreads (which would
@@ -304,15 +295,20 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
     // ---- issue the DMA of stage s into buffer bf ----
     auto issue = [&](int s, int bf) {
         const int k0 = s * kBN;
-        const bool tail = k0 + kBN > L;  // uniform: clamp rows past L to L-1
         const unsigned lb = smem_base + bf * S::STAGE;
+        unsigned voff[NJ];
+        if (k0 + kBN <= L) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            unsigned voff = (unsigned)k0 * dstr[j] + dloff[j];
-            if (tail) voff = (unsigned)min(k0 + drow[j], L - 1) * dstr[j] + dcol[j];
-            dma16(dsb[j], voff, lb + dlds[j]);
+            for (int j = 0; j < NJ; ++j) voff[j] = (unsigned)k0 * dstr[j] + dloff[j];
+        } else {  // last stage: clamp rows past L to L-1 (their keys are masked)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) voff[j] = (unsigned)min(k0 + drow[j], L - 1) * dstr[j] + dcol[j];
         }
+        const int m0v = m0_save();
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) dma16(dsb[j], voff[j], lb + dlds[j]);
         dma4(keff_b, (unsigned)(k0 + lane) * 4u, scid_base + bf * kBN * 4);
+        m0_restore(m0v);
     };
 
     // ---- Q fragments (B operand of S^T = K Q^T): dims kk*16 + 8*hh + [0,8) ----
@@ -346,9 +342,15 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
     }
 
     // ---- online softmax state ----
-    const float c = args.c;
-    const float th = 8.0f / c;  // rescale threshold in raw logit units (2^8)
-    float m_ref = -INFINITY;
+    // Logits are handled in base-2 units, s2 = c * s. With BIAS (fused RoPE) c
+    // is folded into Q in fp32 before its single rounding, and the MFMA itself
+    // returns s2 - m_ref through one extra feature (K side 1, Q side -m_ref,
+    // m_ref kept bf16-exact): no per-logit FMA. Without BIAS (caller-rotated
+    // q/k used as given) s2 - m_ref is one FMA per logit.
+    constexpr bool BIAS = ROPE;
+    const float c = args.c;  // 1 with BIAS
+    float m_ref = 0.f;       // reference max (base 2)
+    bool started = false;    // wave-uniform: m_ref has been set
     float l_run = 0.f;
     f32x16 o[S::NDB];
 #pragma unroll
@@ -358,29 +360,66 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
 
     // K operand row: subtile row ql with bits 2,3 swapped.
     const int krow = (ql & ~12) | ((ql & 4) << 1) | ((ql & 8) >> 1);
-    v8 zero8, one8;
+    v8 zero8, one8, unit8;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) { zero8[t] = (T)0.f; one8[t] = (T)1.0f; }
-
-    // A operand of S^T = K Q^T: K rows, dims kk*16 + 8*hh + [0, 8).
-    auto kop = [&](const char* stage, int ten, int st, int kk) -> v8 {
-        const int cch = 2 * kk + hh;
-        if (cch >= S::NCH) return zero8;  // D = 24: dims [24, 32)
-        const int r = st * 32 + krow;
-        return *reinterpret_cast<const v8*>(stage + ten * S::TILE + r * S::RB + S::swz(r, cch) * 16);
+    for (int t = 0; t < 8; ++t) {
+        zero8[t] = (T)0.f;
+        one8[t] = (T)1.0f;
+        unit8[t] = (T)(t == 0 ? 1.0f : 0.0f);
+    }
+    // Bias feature: an extra K-chunk (K side: 1 at dim 0 of lane half 0) for
+    // D != 24; for D = 24 it is dim 24, inside the zero padding [24, 32).
+    const v8 kbias = hh == 0 ? unit8 : zero8;
+    v8 qbias = zero8;
+    auto set_bias = [&]() {
+        const T nb = (T)(-m_ref);
+        if constexpr (D == 24) {
+            if (hh) {
+                qf[0][1][0] = nb;
+                qf[1][1][0] = nb;
+            }
+        } else {
+            if (hh == 0) qbias[0] = nb;
+        }
     };
-    // A operand of O^T += V^T P^T for d block db: V[key(slot j)][d = db*32 + l%32]
-    // via two ds_read_b64_tr_b16 (each: 4 keys x 4 dims per 16-lane group).
+
+    // Per-lane LDS byte offsets of the MFMA operands inside a tile. The chunk
+    // swizzle repeats every 16 rows, so moving to another subtile or key chunk
+    // only adds a constant.
+    // K operand (A of S^T = K Q^T): row krow, dims kk*16 + 8*hh + [0, 8).
+    int koff[S::NKK];
+#pragma unroll
+    for (int kk = 0; kk < S::NKK; ++kk) {
+        const int cch = 2 * kk + hh;
+        koff[kk] = cch < S::NCH ? krow * S::RB + S::swz(krow, cch) * 16 : 0;
+    }
+    // V operand (A of O^T += V^T P^T) for d block db via ds_read_b64_tr_b16:
+    // lane (group tg, index ti) addresses row 8*(tg>>1) + 4*rr + ti/4 and the
+    // 8-byte chunk 8*db + 4*(tg&1) + ti%4 (clamped into the row when D = 24/16;
+    // those lanes' results are replaced by the ones rows).
     const int tg = lane >> 4, ti = lane & 15;
+    int voffv[S::NDB][2];
+#pragma unroll
+    for (int db = 0; db < S::NDB; ++db) {
+        int e = 8 * db + 4 * (tg & 1) + (ti & 3);
+        if (8 * e >= S::RB) e = ti & 3;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int row = 8 * (tg >> 1) + 4 * rr + (ti >> 2);
+            voffv[db][rr] = row * S::RB + S::swz(row, e >> 1) * 16 + (e & 1) * 8;
+        }
+    }
+
+    auto kop = [&](const char* stage, int ten, int st, int kk) -> v8 {
+        if (2 * kk + hh >= S::NCH) return BIAS ? unit8 : zero8;  // D = 24: dims [24, 32)
+        return *reinterpret_cast<const v8*>(stage + ten * S::TILE + st * 32 * S::RB + koff[kk]);
+    };
     auto vop = [&](const char* stage, int ten, int st, int cc, int db) -> v8 {
         const int d = db * 32 + (lane & 31);
-        int e = 8 * db + 4 * (tg & 1) + (ti & 3);  // 8-byte chunk this lane addresses
-        if (8 * e >= S::RB) e = ti & 3;          // keep addresses in bounds (result unused)
         s4 half[2];
 #pragma unroll
         for (int rr = 0; rr < 2; ++rr) {
-            const int row = st * 32 + 16 * cc + 8 * (tg >> 1) + 4 * rr + (ti >> 2);
-            const char* ptr = stage + ten * S::TILE + row * S::RB + S::swz(row, e >> 1) * 16 + (e & 1) * 8;
+            const char* ptr = stage + ten * S::TILE + (st * 32 + 16 * cc) * S::RB + voffv[db][rr];
             half[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(ptr));
         }
         // Whole-vector bitcast: element-wise i16 -> bf16 inserts are mis-lowered.
@@ -388,20 +427,40 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
         if constexpr (D % 32 == 0) return r8;
         return d < D ? r8 : one8;
     };
+    // S^T of one subtile for pathway pw from preloaded K operands.
+    auto qk = [&](const v8* ka, int pw) -> f32x16 {
+        f32x16 sv;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sv[i] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < S::NKK; ++kk) sv = E::mma(ka[kk], qf[pw][kk], sv);
+        if constexpr (BIAS && D != 24) sv = E::mma(kbias, qbias, sv);
+        return sv;
+    };
 
-    auto update_max = [&](float mx) {
-        if (__any(mx > m_ref + th)) {
-            const float mxa = fmaxf(mx, __shfl_xor(mx, 32));
-            const bool upd = mxa > m_ref + th;
-            const float m_new = upd ? mxa : m_ref;
-            const float alpha = upd ? fast_exp2((m_ref - m_new) * c) : 1.0f;
-            m_ref = m_new;
-            l_run *= alpha;
+    // Reference-max update. `rel` is this lane half's max of s2 - m_ref over
+    // the new logits. Rescales (rarely) when a row max exceeds the reference
+    // by 2^8; the first stage only sets the reference. Returns true if m_ref
+    // moved, with `shift` = new - old (BIAS logits must subtract it).
+    auto update = [&](float rel, float& shift) -> bool {
+        shift = 0.f;
+        const bool need = !started || rel > 8.0f;
+        if (__builtin_amdgcn_ballot_w64(need) == 0) return false;
+        const float ra = fmaxf(rel, __shfl_xor(rel, 32));
+        const bool upd = !started || ra > 8.0f;
+        float m_new = upd ? m_ref + ra : m_ref;
+        if constexpr (BIAS) m_new = (float)(T)m_new;
+        shift = m_new - m_ref;
+        const float alpha = started ? fast_exp2(-shift) : 0.f;
+        l_run *= alpha;
 #pragma unroll
-            for (int db = 0; db < S::NDB; ++db)
+        for (int db = 0; db < S::NDB; ++db)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-        }
+            for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        m_ref = m_new;
+        started = true;
+        if constexpr (BIAS) set_bias();
+        return true;
     };
 
     // One pathway over NS consecutive subtiles starting at subtile st0.
@@ -423,26 +482,31 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
                 for (int db = 0; db < S::NDB; ++db) va[st][cc][db] = vop(stage, 2 + pw, st0 + st, cc, db);
         f32x16 sv[NS];
 #pragma unroll
-        for (int st = 0; st < NS; ++st) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sv[st][i] = 0.f;
-#pragma unroll
-            for (int kk = 0; kk < S::NKK; ++kk) sv[st] = E::mma(ka[st][kk], qf[pw][kk], sv[st]);
-        }
+        for (int st = 0; st < NS; ++st) sv[st] = qk(ka[st], pw);
         float mx = sv[0][0];
 #pragma unroll
         for (int st = 0; st < NS; ++st)
 #pragma unroll
             for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sv[st][i]);
-        update_max(mx);
-        const float mc = m_ref * c;
+        float shift;
+        const bool moved = update(BIAS ? mx : fmaf(mx, c, -m_ref), shift);
+        if constexpr (BIAS) {
+            if (moved) {
+#pragma unroll
+                for (int st = 0; st < NS; ++st)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) sv[st][i] -= shift;
+            }
+        }
+        const float mc = m_ref;
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 float pr[8];
 #pragma unroll
-                for (int t = 0; t < 8; ++t) pr[t] = fast_exp2(fmaf(sv[st][8 * cc + t], c, -mc));
+                for (int t = 0; t < 8; ++t)
+                    pr[t] = fast_exp2(BIAS ? sv[st][8 * cc + t] : fmaf(sv[st][8 * cc + t], c, -mc));
                 const v8 pb = pack8<T>(pr);
                 if constexpr (!S::SUM_MFMA) {
 #pragma unroll
@@ -456,14 +520,14 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
 
     // Both pathways on one subtile, selected per element; handles padded keys.
     auto general = [&](const char* stage, const int* cid, int st, int k0) {
-        f32x16 ss, sm, sv;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) { ss[i] = 0.f; sm[i] = 0.f; }
+        v8 ks[S::NKK], km[S::NKK];
 #pragma unroll
         for (int kk = 0; kk < S::NKK; ++kk) {
-            ss = E::mma(kop(stage, 0, st, kk), qf[0][kk], ss);
-            sm = E::mma(kop(stage, 1, st, kk), qf[1][kk], sm);
+            ks[kk] = kop(stage, 0, st, kk);
+            km[kk] = kop(stage, 1, st, kk);
         }
+        const f32x16 ss = qk(ks, 0), sm = qk(km, 1);
+        f32x16 sv;
         bool same[16];
         // keys of slot i: st*32 + 16*(i/8) + 8*hh + i%8
 #pragma unroll
@@ -491,15 +555,22 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
         float mx = sv[0];
 #pragma unroll
         for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
-        update_max(mx);
-        const float mc = m_ref * c;
+        float shift;
+        const bool moved = update(BIAS ? mx : fmaf(mx, c, -m_ref), shift);
+        if constexpr (BIAS) {
+            if (moved) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sv[i] -= shift;
+            }
+        }
+        const float mc = m_ref;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
             v8 ps, pm;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 const int i = 8 * cc + t;
-                const T pv = (T)fast_exp2(fmaf(sv[i], c, -mc));
+                const T pv = (T)fast_exp2(BIAS ? sv[i] : fmaf(sv[i], c, -mc));
                 ps[t] = same[i] ? pv : (T)0.f;
                 pm[t] = same[i] ? (T)0.f : pv;
             }
@@ -528,8 +599,23 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
         return 2;
     };
 
+    // Pathway codes of 64 consecutive 32-key subtiles starting at kb0, as two
+    // bit masks (bit k of mlo / mhi = low / high bit of subtile kb0 + k).
+    uint64_t mlo = 0, mhi = 0;
+    auto load_modes = [&](int kb0) {
+        const int kb = kb0 + lane;
+        int code = 3;
+        if (kb < Lp / 32) {
+            const int4 sm = ksum_b[kb];
+            code = subtile_mode(sm.x, sm.y, sm.z);
+        }
+        mlo = __builtin_amdgcn_ballot_w64(code & 1);
+        mhi = __builtin_amdgcn_ballot_w64((code >> 1) & 1);
+    };
+
     // ---- main loop over stages ----
     const int nst = (L + kBN - 1) / kBN;
+    load_modes(0);  // before any copy is in flight (its wait drains vmcnt)
 #pragma unroll
     for (int t = 0; t < NBUF - 1; ++t)
         if (t < nst) issue(t, t);
@@ -544,10 +630,10 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
         stage_barrier();
         if (s + NBUF - 1 < nst) issue(s + NBUF - 1, (s + NBUF - 1) % NBUF);
 
-        const int4 sa = sload4(ksum_b + 2 * s);
-        const int4 sb = sload4(ksum_b + 2 * s + 1);
-        const int m0 = subtile_mode(sa.x, sa.y, sa.z);
-        const int m1 = subtile_mode(sb.x, sb.y, sb.z);
+        if (s > 0 && (s & 31) == 0) load_modes(2 * s);
+        const int sub = (2 * s) & 63;
+        const int m0 = (int)((mlo >> sub) & 1) | (int)(((mhi >> sub) & 1) << 1);
+        const int m1 = (int)((mlo >> (sub + 1)) & 1) | (int)(((mhi >> (sub + 1)) & 1) << 1);
         const char* stage = smem + bf * S::STAGE;
         const int* cid = &scid[wave][bf][0];
         const int k0 = s * kBN;
@@ -592,7 +678,7 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
             }
         if (p.lse && hh == 0) {
             p.lse[((int64_t)b * H + h) * L + q] =
-                l_tot > 0.f ? m_ref * args.lse_mul + logf(l_tot) : -INFINITY;
+                l_tot > 0.f ? (m_ref + __log2f(l_tot)) * kLn2 : -INFINITY;
         }
     }
 }
@@ -648,10 +734,11 @@ static hipError_t dispatch_fwd_t(FwdArgs& a, hipStream_t s) {
 hipError_t launch_fwd16(const mpattn_fwd_params& p, hipStream_t stream) {
     FwdArgs a;
     a.p = p;
+    // Fused RoPE folds scale * log2(e) into Q; caller-rotated q keeps its
+    // exact values and the factor is applied per logit.
     const bool fused = p.rope == MPATTN_ROPE_FUSED;
-    a.qmul = fused ? p.scale : 1.0f;
-    a.c = fused ? kLog2e : p.scale * kLog2e;
-    a.lse_mul = fused ? 1.0f : p.scale;
+    a.qmul = fused ? p.scale * kLog2e : 1.0f;
+    a.c = fused ? 1.0f : p.scale * kLog2e;
     if (p.dtype == MPATTN_BF16) return dispatch_fwd_t<bf16_t>(a, stream);
     return dispatch_fwd_t<fp16_t>(a, stream);
 }
