@@ -223,8 +223,16 @@ __device__ __forceinline__ void stage_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+#ifndef MPATTN_FWD_WAVES
+#define MPATTN_FWD_WAVES 4  // register budget: wavefronts per SIMD
+#endif
+#ifndef MPATTN_FWD_NBUF32
+#define MPATTN_FWD_NBUF32 2  // LDS stages in flight for D <= 32
+#endif
+
 template <typename T, int D, int W, int NBUF, bool ROPE, bool DENSE>
-__global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(MPATTN_FWD_WAVES)))
+void fwd_kernel(const FwdArgs args) {
     using S = FwdShape<D>;
     using E = Elt<T>;
     typedef typename E::v8 v8;
@@ -347,7 +355,10 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
     // returns s2 - m_ref through one extra feature (K side 1, Q side -m_ref,
     // m_ref kept bf16-exact): no per-logit FMA. Without BIAS (caller-rotated
     // q/k used as given) s2 - m_ref is one FMA per logit.
-    constexpr bool BIAS = ROPE;
+    // The bias feature costs one more MFMA on each subtile's dependency chain
+    // (QK -> bias -> max -> exp); measured on MI355X at the 150M shape it is
+    // slower (182 us vs 153 us) than one FMA per logit, so it stays off.
+    constexpr bool BIAS = false;
     const float c = args.c;  // 1 with BIAS
     float m_ref = 0.f;       // reference max (base 2)
     bool started = false;    // wave-uniform: m_ref has been set
@@ -686,7 +697,7 @@ __global__ __launch_bounds__(W * 64) void fwd_kernel(const FwdArgs args) {
 template <typename T, int D, bool ROPE, bool DENSE>
 static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     constexpr int W = 4;
-    constexpr int NBUF = D <= 32 ? 3 : 2;
+    constexpr int NBUF = D <= 32 ? MPATTN_FWD_NBUF32 : 2;
     const mpattn_fwd_params& p = a.p;
     const int Lp = round_up(p.L, kBN);
     a.Lp = Lp;
