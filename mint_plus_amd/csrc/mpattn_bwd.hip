@@ -1,17 +1,941 @@
-// Backward multi-pathway attention (placeholder until the kernels land).
+// Backward multi-pathway attention for gfx950 (16-bit inputs, fp32 accumulate).
+//
+// Gradients of the op defined in include/mpattn.h, following the softmax
+// backward of the reference eager path (autograd through
+// mint_plus/models/modules_plus.py:178-194 and attention.py:186-236):
+//
+//   P_ij  = exp(s_ij - LSE_i)                 (LSE saved by the forward)
+//   dV_j  = sum_i P_ij dO_i                  (into V_self or V_multi by pathway)
+//   dP_ij = dO_i . V_sel(ij),j
+//   dS_ij = P_ij (dP_ij - Delta_i),           Delta_i = dO_i . O_i
+//   dQ_i  = scale sum_j dS_ij K_sel,j ;  dK_j = scale sum_i dS_ij Q_sel,i
+//   and R_p^T applied to dQ_self / dK_self with fused RoPE.
+//
+// This is the exact gradient; the reference's Triton backward
+// (mint_plus/models/kernels/multi_pathway_attention_bwd.py:123-271) takes the
+// softmax row sum per key tile and applies the scale twice, and is not
+// followed. No atomics: dK/dV and dQ come from separate kernels, so results
+// are bitwise reproducible.
+//
+// Launches:
+//  1. bwd_prep_kernel: chain staging for keys (as the forward) and queries,
+//     Delta and LSE*log2(e) per query, RoPE-rotated Q_self/K_self.
+//  2. bwd_dkdv_kernel (key-stationary): each wavefront keeps K and V of 32
+//     keys in registers (MFMA B operands) and streams 64-query stages of
+//     Q_self, Q_multi, dO through LDS. S and dP come out with lane = key and
+//     slot = query (query rows read bit-2/3-swapped), which is directly the A
+//     operand of dV += P^T dO and dK += dS^T Q; dO^T and Q^T are transpose
+//     reads of the row-major tiles.
+//  3. bwd_dq_kernel (query-stationary): the forward's structure plus
+//     dP^T = V dO^T and dQ^T += K^T dS^T.
+#include <type_traits>
+
 #include "mpattn_common.h"
 
 namespace mpattn {
+
+constexpr int kBS = 64;  // rows per LDS stage
+
+static inline int rup(int x, int m) { return (x + m - 1) / m * m; }
+
+// Workspace layout (offsets 256-byte aligned), Lp = L rounded up to 64:
+//   lse2  f32   [B][H][Lp]   LSE * log2(e); +inf past L
+//   delta f32   [B][H][Lp]   dO . O; 0 past L
+//   keff  int32 [B][Lp]      key chain id, kPadChain for padded / past L
+//   ksum  int32 [B][Lp/32][4] key blocks: min, max chain (valid keys), #padded
+//   qcid  int32 [B][Lp]      query chain id (queries past L: 0)
+//   qsum  int32 [B][Lp/32][4] query blocks: min, max chain (queries < L)
+//   qrot, krot T [B][H][Lp][D]  RoPE-rotated Q_self / K_self (fused RoPE)
+struct BwdWs {
+    int64_t lse2, delta, keff, ksum, qcid, qsum, qrot, krot, total;
+};
+
+static inline BwdWs bwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
+    const int64_t Lp = rup(L, kBS);
+    auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+    BwdWs w;
+    w.lse2 = 0;
+    w.delta = al(w.lse2 + (int64_t)B * H * Lp * 4);
+    w.keff = al(w.delta + (int64_t)B * H * Lp * 4);
+    w.ksum = al(w.keff + (int64_t)B * Lp * 4);
+    w.qcid = al(w.ksum + (int64_t)B * (Lp / 32) * 16);
+    w.qsum = al(w.qcid + (int64_t)B * Lp * 4);
+    w.qrot = al(w.qsum + (int64_t)B * (Lp / 32) * 16);
+    const int64_t rot = rope ? (int64_t)B * H * Lp * D * esize : 0;
+    w.krot = al(w.qrot + rot);
+    w.total = al(w.krot + rot);
+    return w;
+}
+
 int64_t bwd_workspace_bytes(int B, int H, int L, int D) {
-    (void)D;
-    return (int64_t)B * H * L * 4;
+    // Sized for the largest element type and fused RoPE: callers allocate
+    // once regardless of the mode.
+    return bwd_ws_layout(B, H, L, D, 4, true).total;
 }
+
+struct BwdArgs {
+    mpattn_bwd_params p;
+    const float* lse2;
+    const float* delta;
+    const int* keff;
+    const int* ksum;
+    const int* qcid;
+    const int* qsum;
+    const void* qrot;
+    const void* krot;
+    int Lp;
+    float c;  // scale * log2(e)
+};
+
+// ---------------------------------------------------------------------------
+// Prep: chain staging, Delta / LSE2 rows, RoPE of Q_self and K_self.
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool ROPE, bool DENSE>
+__global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* lse2, float* delta,
+                                                       int* keff, int* ksum, int* qcid, int* qsum,
+                                                       T* qrot, T* krot, int nchain, int nrow) {
+    typedef typename Elt<T>::v8 v8;
+    const mpattn_bwd_params& p = a.p;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int L = p.L, Lp = a.Lp;
+    const int bid = blockIdx.x;
+    if (bid < nchain) {
+        const int ngrp = Lp / 64;
+        const int gid = bid * 4 + wave;
+        if (gid >= p.B * ngrp) return;
+        const int b = gid / ngrp, k0 = (gid % ngrp) * 64;
+        const int kg = k0 + lane;
+        const int cid = kg < L ? (DENSE ? 0 : p.chain_id[(int64_t)b * L + kg]) : 0;
+        const bool pad = kg >= L || (p.key_pad && p.key_pad[(int64_t)b * L + kg]);
+        const int ke = pad ? kPadChain : cid;
+        keff[(int64_t)b * Lp + kg] = ke;
+        qcid[(int64_t)b * Lp + kg] = cid;
+        const int hh = lane >> 5;
+        {
+            const int mn = half_min_i(pad ? INT32_MAX : cid);
+            const int mx = half_max_i(pad ? INT32_MIN : cid);
+            const uint64_t padm = __ballot(pad);
+            if ((lane & 31) == 0) {
+                int* o = ksum + ((int64_t)b * (Lp / 32) + (k0 >> 5) + hh) * 4;
+                o[0] = mn;
+                o[1] = mx;
+                o[2] = __popcll(hh ? (padm >> 32) : (padm & 0xffffffffull));
+                o[3] = 0;
+            }
+        }
+        {
+            const bool qv = kg < L;
+            const int mn = half_min_i(qv ? cid : INT32_MAX);
+            const int mx = half_max_i(qv ? cid : INT32_MIN);
+            const uint64_t inval = __ballot(!qv);
+            if ((lane & 31) == 0) {
+                int* o = qsum + ((int64_t)b * (Lp / 32) + (k0 >> 5) + hh) * 4;
+                o[0] = mn;
+                o[1] = mx;
+                o[2] = __popcll(hh ? (inval >> 32) : (inval & 0xffffffffull));
+                o[3] = 0;
+            }
+        }
+        return;
+    }
+    if (bid < nchain + nrow) {
+        // One thread per (b, h, row < Lp): Delta and LSE2.
+        const int64_t row = (int64_t)(bid - nchain) * 256 + tid;
+        if (row >= (int64_t)p.B * p.H * Lp) return;
+        const int t = (int)(row % Lp);
+        const int bh = (int)(row / Lp);
+        const int b = bh / p.H, h = bh % p.H;
+        float dl = 0.f, l2 = INFINITY;
+        if (t < L) {
+            const T* orow = (const T*)p.out.ptr + b * p.out.stride_b + h * p.out.stride_h +
+                            (int64_t)t * p.out.stride_t;
+            const T* grow = (const T*)p.grad_out.ptr + b * p.grad_out.stride_b +
+                            h * p.grad_out.stride_h + (int64_t)t * p.grad_out.stride_t;
+#pragma unroll
+            for (int d0 = 0; d0 < D; d0 += 8) {
+                float x[8], y[8];
+                load8f<T>(orow, d0, x);
+                load8f<T>(grow, d0, y);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) dl += x[u] * y[u];
+            }
+            const float lse = p.lse[((int64_t)b * p.H + h) * L + t];
+            // A row whose keys are all padded has LSE = -inf and no probabilities.
+            l2 = lse == -INFINITY ? INFINITY : lse * kLog2e;
+        }
+        lse2[row] = l2;
+        delta[row] = dl;
+        return;
+    }
+    if constexpr (ROPE) {
+        // Rotate rows of Q_self (first half of items) and K_self (second half).
+        const int64_t rows = (int64_t)p.B * p.H * Lp;
+        int64_t item = (int64_t)(bid - nchain - nrow) * 256 + tid;
+        if (item >= 2 * rows) return;
+        const bool isk = item >= rows;
+        const int64_t row = isk ? item - rows : item;
+        const int t = (int)(row % Lp);
+        const int bh = (int)(row / Lp);
+        const int b = bh / p.H, h = bh % p.H;
+        const mpattn_tensor& src_t = isk ? p.k_self : p.q_self;
+        const T* src = (const T*)src_t.ptr + b * src_t.stride_b + h * src_t.stride_h + (int64_t)t * src_t.stride_t;
+        T* dst = (isk ? krot : qrot) + row * D;
+#pragma unroll
+        for (int d0 = 0; d0 < D; d0 += 8) {
+            float x[8];
+            if (t < L) load8_rot<T, D>(src, p.rope_cos, p.rope_sin, t, d0, 1.0f, true, x);
+            else
+                for (int u = 0; u < 8; ++u) x[u] = 0.f;
+            *reinterpret_cast<v8*>(dst + d0) = pack8<T>(x);
+        }
+    }
+}
+
+// Shapes shared by the two gradient kernels.
+template <int D> struct BwdShape {
+    static constexpr int DP = D <= 16 ? 16 : (D <= 32 ? 32 : 64);  // MFMA K over head dims
+    static constexpr int NKK = DP / 16;
+    static constexpr int NDB = DP <= 32 ? 1 : 2;  // 32-column blocks of head dims
+};
+
+// Stage the wave's 32 x D fp32 result tile `acc` (layout: lane l holds column
+// db*32 + l%32 of rows 8*(i/4) + 4*hh + i%4, or the transposed layout when
+// TRANS) through LDS scratch and write rows r0 .. r0+31 of `dst` (rows >= L
+// skipped), optionally rotated back by RoPE (R_p^T, p = row index) and scaled.
+template <typename T, int D, bool TRANS>
+__device__ void store_rows(const f32x16* acc, float* scratch, const mpattn_tensor& dst, int b, int h,
+                           int r0, int L, float mul, bool rope, const float* cos_tab,
+                           const float* sin_tab) {
+    using BS = BwdShape<D>;
+    typedef typename Elt<T>::v8 v8;
+    const int lane = threadIdx.x & 63, hh = lane >> 5, ql = lane & 31;
+    constexpr int LD = BS::NDB * 32 + 1;  // padded row stride (floats)
+#pragma unroll
+    for (int db = 0; db < BS::NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int m = 8 * (i / 4) + 4 * hh + (i % 4);
+            // TRANS: accumulator rows are head dims, columns rows of dst.
+            const int row = TRANS ? ql : m;
+            const int col = TRANS ? db * 32 + m : db * 32 + ql;
+            scratch[row * LD + col] = acc[db][i] * mul;
+        }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    // lane -> (row, 8-wide chunk) items
+    constexpr int NCHK = D / 8;
+    for (int it = lane; it < 32 * NCHK; it += 64) {
+        const int row = it / NCHK, d0 = (it % NCHK) * 8;
+        const int r = r0 + row;
+        if (r >= L) continue;
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = scratch[row * LD + d0 + u];
+        if (rope) {
+            constexpr int H2 = D / 2;
+            const float* cr = cos_tab + (int64_t)r * H2;
+            const float* sr = sin_tab + (int64_t)r * H2;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int d = d0 + u;
+                const bool lo = d < H2;
+                const int dp = lo ? d + H2 : d - H2;
+                const int fi = lo ? d : dp;
+                const float y = scratch[row * LD + dp];
+                // transpose of x*cos + rotate_half(x)*sin
+                x[u] = x[u] * cr[fi] + (lo ? y : -y) * sr[fi];
+            }
+        }
+        T* out = (T*)dst.ptr + b * dst.stride_b + h * dst.stride_h + (int64_t)r * dst.stride_t;
+        *reinterpret_cast<v8*>(out + d0) = pack8<T>(x);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV: key-stationary.
+// ---------------------------------------------------------------------------
+template <typename T, int D, int W, bool ROPE, bool DENSE>
+__global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
+    using TS = TileShape<D>;
+    using BS = BwdShape<D>;
+    using E = Elt<T>;
+    typedef typename E::v8 v8;
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    constexpr int NTEN = 3;  // Q_self, Q_multi, dO
+    constexpr int TOT = NTEN * TS::NI;
+    constexpr int NJ = (TOT + W - 1) / W;  // copies per wave (the last may be idle)
+    constexpr int AUX = 4 * kBS * 4;  // lse2, delta, qcid (+ spare) floats/ints
+    constexpr int STAGE = NTEN * TS::TILE + AUX;
+    constexpr int NBUF = 2;
+    const mpattn_bwd_params& p = a.p;
+
+    __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE > W * 32 * 65 * 4 ? NBUF * STAGE
+                                                                                   : W * 32 * 65 * 4];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ql = lane & 31, hh = lane >> 5;
+    const int L = p.L, H = p.H, Lp = a.Lp;
+    const int nkb = (L + 32 * W - 1) / (32 * W);
+    const int g = xcd_remap(blockIdx.x, gridDim.x);
+    const int kblk = g % nkb, bh = g / nkb;
+    const int b = bh / H, h = bh % H;
+    const int kw0 = kblk * 32 * W + wave * 32;  // first key of this wave
+    const int key = kw0 + ql;                   // this lane's key (B operand column)
+
+    auto base = [&](const mpattn_tensor& t) { return (const T*)t.ptr + b * t.stride_b + h * t.stride_h; };
+    const T* const qs_p = ROPE ? (const T*)a.qrot + (int64_t)bh * Lp * D : base(p.q_self);
+    const int64_t qs_t = ROPE ? D : p.q_self.stride_t;
+    const T* const qm_p = base(p.q_multi);
+    const T* const do_p = base(p.grad_out);
+    const T* const ks_p = ROPE ? (const T*)a.krot + (int64_t)bh * Lp * D : base(p.k_self);
+    const int64_t ks_t = ROPE ? D : p.k_self.stride_t;
+    const T* const km_p = base(p.k_multi);
+    const T* const vs_p = base(p.v_self);
+    const T* const vm_p = base(p.v_multi);
+    const float* const lse2_bh = a.lse2 + (int64_t)bh * Lp;
+    const float* const delta_bh = a.delta + (int64_t)bh * Lp;
+    const int* const qcid_b = a.qcid + (int64_t)b * Lp;
+    const int4* const qsum_b = reinterpret_cast<const int4*>(a.qsum) + (int64_t)b * (Lp / 32);
+
+    // ---- key-side registers: B operands K[key][dims kk*16 + 8*hh + (0..7)] ----
+    v8 kf[2][BS::NKK], vf[2][BS::NKK];
+    const bool kin = key < L;
+#pragma unroll
+    for (int kk = 0; kk < BS::NKK; ++kk) {
+        const int d0 = kk * 16 + hh * 8;
+        float x[8];
+#pragma unroll
+        for (int pw = 0; pw < 2; ++pw) {
+            const T* kr = pw == 0 ? ks_p + (int64_t)key * ks_t : km_p + (int64_t)key * p.k_multi.stride_t;
+            const T* vr = pw == 0 ? vs_p + (int64_t)key * p.v_self.stride_t : vm_p + (int64_t)key * p.v_multi.stride_t;
+            if (kin && d0 < D) load8f<T>(kr, d0, x);
+            else for (int u = 0; u < 8; ++u) x[u] = 0.f;
+            kf[pw][kk] = pack8<T>(x);
+            if (kin && d0 < D) load8f<T>(vr, d0, x);
+            else for (int u = 0; u < 8; ++u) x[u] = 0.f;
+            vf[pw][kk] = pack8<T>(x);
+        }
+    }
+    const int ckey = kin ? a.keff[(int64_t)b * Lp + key] : kPadChain;  // kPadChain if padded
+    const bool kvalid = ckey != kPadChain;
+    const int kc_min = __builtin_amdgcn_readfirstlane(wave_min_i(kvalid ? ckey : INT32_MAX));
+    const int kc_max = __builtin_amdgcn_readfirstlane(wave_max_i(kvalid ? ckey : INT32_MIN));
+    const bool any_pad = __builtin_amdgcn_ballot_w64(!kvalid) != 0;
+
+    // ---- accumulators: [0] self, [1] multimer ----
+    f32x16 dv[2][BS::NDB], dk[2][BS::NDB];
+#pragma unroll
+    for (int pw = 0; pw < 2; ++pw)
+#pragma unroll
+        for (int db = 0; db < BS::NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dv[pw][db][i] = dk[pw][db][i] = 0.f;
+
+    // ---- DMA plan (as the forward) ----
+    const char* dsb[NJ];
+    unsigned dstr[NJ], dlds[NJ], dloff[NJ];
+    auto dma_slot = [&](int j, int& r, int& cb) {
+        const int slot = ((wave + j * W) % TS::NI) * 64 + lane;
+        r = slot / TS::NCH;
+        cb = TS::swz(r, slot % TS::NCH) * 16;
+    };
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int ins = min(wave + j * W, TOT - 1);
+        const int ten = ins / TS::NI, part = ins % TS::NI;
+        int r, cb;
+        dma_slot(j, r, cb);
+        const T* tb = ten == 0 ? qs_p : ten == 1 ? qm_p : do_p;
+        const int64_t ts = ten == 0 ? qs_t : ten == 1 ? p.q_multi.stride_t : p.grad_out.stride_t;
+        dsb[j] = (const char*)tb;
+        dstr[j] = (unsigned)(ts * (int64_t)sizeof(T));
+        dlds[j] = ten * TS::TILE + part * 1024;
+        dloff[j] = r * dstr[j] + cb;
+    }
+    const unsigned smem_base = lds_addr(smem);
+    // aux copy of this wave: 0 lse2, 1 delta, 2 qcid, 3 (spare: qcid again)
+    const int aux = wave & 3;
+    const char* aux_src = aux == 0 ? (const char*)lse2_bh : aux == 1 ? (const char*)delta_bh : (const char*)qcid_b;
+    auto issue = [&](int s, int bf) {
+        const int q0 = s * kBS;
+        const unsigned lb = smem_base + bf * STAGE;
+        unsigned voff[NJ];
+        if (q0 + kBS <= L) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) voff[j] = (unsigned)q0 * dstr[j] + dloff[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                int r, cb;
+                dma_slot(j, r, cb);
+                voff[j] = (unsigned)min(q0 + r, L - 1) * dstr[j] + cb;
+            }
+        }
+        const int m0v = m0_save();
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+            if (TOT % W == 0 || wave + j * W < TOT) dma16(dsb[j], voff[j], lb + dlds[j]);
+        dma4(aux_src, (unsigned)(q0 + lane) * 4u, lb + NTEN * TS::TILE + aux * kBS * 4);
+        m0_restore(m0v);
+    };
+
+    // ---- operand readers ----
+    const int qrow = swapped_row(ql);
+    int roff[BS::NKK];
+#pragma unroll
+    for (int kk = 0; kk < BS::NKK; ++kk) {
+        const int cch = 2 * kk + hh;
+        roff[kk] = cch < TS::NCH ? qrow * TS::RB + TS::swz(qrow, cch) * 16 : 0;
+    }
+    const int tg = lane >> 4, ti = lane & 15;
+    int toff[BS::NDB][2];
+#pragma unroll
+    for (int db = 0; db < BS::NDB; ++db) {
+        int e = 8 * db + 4 * (tg & 1) + (ti & 3);
+        if (8 * e >= TS::RB) e = ti & 3;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int row = 8 * (tg >> 1) + 4 * rr + (ti >> 2);
+            toff[db][rr] = row * TS::RB + TS::swz(row, e >> 1) * 16 + (e & 1) * 8;
+        }
+    }
+    v8 zero8;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) zero8[t] = (T)0.f;
+    // A operand: rows (queries) of tile `ten`, bit-swapped order.
+    auto rop = [&](const char* stage, int ten, int st, int kk) -> v8 {
+        if (2 * kk + hh >= TS::NCH) return zero8;
+        return *reinterpret_cast<const v8*>(stage + ten * TS::TILE + st * 32 * TS::RB + roff[kk]);
+    };
+    // B operand: tile^T, lane -> column d = db*32 + l%32, 8 rows 16*cc + 8*hh + j.
+    auto top = [&](const char* stage, int ten, int st, int cc, int db) -> v8 {
+        s4 half[2];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const char* ptr = stage + ten * TS::TILE + (st * 32 + 16 * cc) * TS::RB + toff[db][rr];
+            half[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(ptr));
+        }
+        const v8 r8 = __builtin_bit_cast(v8, __builtin_shufflevector(half[0], half[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        if constexpr (D % 32 == 0) return r8;
+        return db * 32 + (lane & 31) < D ? r8 : zero8;
+    };
+    // per-slot query data (slot i -> query st*32 + 16*(i/8) + 8*hh + i%8)
+    auto aux16 = [&](const char* stage, int which, int st, float* out) {
+        const float* base_f = (const float*)(stage + NTEN * TS::TILE + which * kBS * 4);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const int ql0 = st * 32 + 16 * cc + 8 * hh;
+            const f32x4 x0 = *reinterpret_cast<const f32x4*>(base_f + ql0);
+            const f32x4 x1 = *reinterpret_cast<const f32x4*>(base_f + ql0 + 4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                out[8 * cc + t] = x0[t];
+                out[8 * cc + 4 + t] = x1[t];
+            }
+        }
+    };
+
+    const float c = a.c;
+    auto mma_kloop = [&](const v8* aop, const v8* bop) {
+        f32x16 acc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < BS::NKK; ++kk) acc = E::mma(aop[kk], bop[kk], acc);
+        return acc;
+    };
+
+    // One subtile of 32 queries; mode 0/1: pure pathway, 2: both pathways.
+    auto subtile = [&](const char* stage, int st, int mode, int q0) {
+        float l2[16], dl[16];
+        aux16(stage, 0, st, l2);
+        aux16(stage, 1, st, dl);
+        v8 qa[2][BS::NKK], doa[BS::NKK];
+#pragma unroll
+        for (int kk = 0; kk < BS::NKK; ++kk) doa[kk] = rop(stage, 2, st, kk);
+        f32x16 pm, dsm;  // P and dS in the selected pathway, per slot
+        bool same[16];
+        if (mode != 2) {
+            const int pw = mode;
+#pragma unroll
+            for (int kk = 0; kk < BS::NKK; ++kk) qa[0][kk] = rop(stage, pw, st, kk);
+            const f32x16 sv = mma_kloop(qa[0], pw == 0 ? kf[0] : kf[1]);
+            const f32x16 dp = mma_kloop(doa, pw == 0 ? vf[0] : vf[1]);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                pm[i] = fast_exp2(fmaf(sv[i], c, -l2[i]));
+                dsm[i] = pm[i] * (dp[i] - dl[i]);
+                same[i] = pw == 0;
+            }
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < BS::NKK; ++kk) {
+                qa[0][kk] = rop(stage, 0, st, kk);
+                qa[1][kk] = rop(stage, 1, st, kk);
+            }
+            const f32x16 ss = mma_kloop(qa[0], kf[0]);
+            const f32x16 sm = mma_kloop(qa[1], kf[1]);
+            const f32x16 dps = mma_kloop(doa, vf[0]);
+            const f32x16 dpm = mma_kloop(doa, vf[1]);
+            int qc[16];
+            {
+                float tmp[16];
+                aux16(stage, 2, st, tmp);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) qc[i] = __builtin_bit_cast(int, tmp[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                bool sm_;
+                if constexpr (DENSE) {
+                    const int qg = q0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8);
+                    sm_ = !(qg < L && kin &&
+                            p.chain_mask[(int64_t)b * p.mask_stride_b + (int64_t)qg * p.mask_stride_q +
+                                         (int64_t)key * p.mask_stride_k] != 0);
+                } else {
+                    sm_ = qc[i] == ckey;
+                }
+                same[i] = sm_;
+                const float s = sm_ ? ss[i] : sm[i];
+                const float dp = sm_ ? dps[i] : dpm[i];
+                pm[i] = kvalid ? fast_exp2(fmaf(s, c, -l2[i])) : 0.f;
+                dsm[i] = pm[i] * (dp - dl[i]);
+            }
+        }
+        // dV_pw += P^T dO ; dK_pw += dS^T Q_pw, per 16-query chunk cc
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            v8 ps, pmv, dss, dsmv;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int i = 8 * cc + t;
+                const T pv = (T)pm[i], dv_ = (T)dsm[i];
+                ps[t] = same[i] ? pv : (T)0.f;
+                pmv[t] = same[i] ? (T)0.f : pv;
+                dss[t] = same[i] ? dv_ : (T)0.f;
+                dsmv[t] = same[i] ? (T)0.f : dv_;
+            }
+#pragma unroll
+            for (int db = 0; db < BS::NDB; ++db) {
+                const v8 dot = top(stage, 2, st, cc, db);
+                if (mode != 1) {
+                    dv[0][db] = E::mma(ps, dot, dv[0][db]);
+                    dk[0][db] = E::mma(dss, top(stage, 0, st, cc, db), dk[0][db]);
+                }
+                if (mode != 0) {
+                    dv[1][db] = E::mma(pmv, dot, dv[1][db]);
+                    dk[1][db] = E::mma(dsmv, top(stage, 1, st, cc, db), dk[1][db]);
+                }
+            }
+        }
+    };
+
+    auto qmode = [&](int qmin, int qmax, int ninval) {
+        if (ninval == 32) return 3;
+        if (!DENSE && !any_pad) {
+            if (qmin == qmax && kc_min == kc_max && qmin == kc_min) return 0;
+            if (qmax < kc_min || qmin > kc_max) return 1;
+        }
+        return 2;
+    };
+
+    // Every wave runs every stage, also one whose keys are all padded: the
+    // stage copies are split over the waves and the barriers are block-wide.
+    const int nst = (L + kBS - 1) / kBS;
+    issue(0, 0);
+    for (int s = 0; s < nst; ++s) {
+        const int bf = s & 1;
+        wait_vm<0>();
+        stage_barrier();
+        if (s + 1 < nst) issue(s + 1, bf ^ 1);
+        const char* stage = smem + bf * STAGE;
+        const int q0 = s * kBS;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const int4 qs = qsum_b[2 * s + st];
+            const int md = qmode(__builtin_amdgcn_readfirstlane(qs.x), __builtin_amdgcn_readfirstlane(qs.y),
+                                 __builtin_amdgcn_readfirstlane(qs.z));
+            if (md == 0) subtile(stage, st, 0, q0);
+            else if (md == 1) subtile(stage, st, 1, q0);
+            else if (md == 2) subtile(stage, st, 2, q0);
+        }
+    }
+    wait_vm<0>();
+    stage_barrier();  // stage buffers become epilogue scratch
+
+    float* scratch = (float*)(smem + wave * 32 * 65 * 4);
+    const float scale = p.scale;
+    store_rows<T, D, false>(dv[0], scratch, p.dv_self, b, h, kw0, L, 1.0f, false, nullptr, nullptr);
+    store_rows<T, D, false>(dv[1], scratch, p.dv_multi, b, h, kw0, L, 1.0f, false, nullptr, nullptr);
+    store_rows<T, D, false>(dk[0], scratch, p.dk_self, b, h, kw0, L, scale, ROPE, p.rope_cos, p.rope_sin);
+    store_rows<T, D, false>(dk[1], scratch, p.dk_multi, b, h, kw0, L, scale, false, nullptr, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// dQ: query-stationary.
+// ---------------------------------------------------------------------------
+template <typename T, int D, int W, bool ROPE, bool DENSE>
+__global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
+    using TS = TileShape<D>;
+    using BS = BwdShape<D>;
+    using E = Elt<T>;
+    typedef typename E::v8 v8;
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    constexpr int NTEN = 4;  // K_self, K_multi, V_self, V_multi
+    constexpr int TOT = NTEN * TS::NI;
+    constexpr int NJ = (TOT + W - 1) / W;  // copies per wave (the last may be idle)
+    constexpr int STAGE = NTEN * TS::TILE;
+    constexpr int NBUF = 2;
+    const mpattn_bwd_params& p = a.p;
+
+    __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE > W * 32 * 65 * 4 ? NBUF * STAGE
+                                                                                   : W * 32 * 65 * 4];
+    __shared__ __attribute__((aligned(16))) int scid[W][NBUF][kBS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ql = lane & 31, hh = lane >> 5;
+    const int L = p.L, H = p.H, Lp = a.Lp;
+    const int nqb = (L + 32 * W - 1) / (32 * W);
+    const int g = xcd_remap(blockIdx.x, gridDim.x);
+    const int qblk = g % nqb, bh = g / nqb;
+    const int b = bh / H, h = bh % H;
+    const int qw0 = qblk * 32 * W + wave * 32;
+    const int q = qw0 + ql;
+    const bool qin = q < L;
+
+    auto base = [&](const mpattn_tensor& t) { return (const T*)t.ptr + b * t.stride_b + h * t.stride_h; };
+    const T* const qs_p = ROPE ? (const T*)a.qrot + (int64_t)bh * Lp * D : base(p.q_self);
+    const int64_t qs_t = ROPE ? D : p.q_self.stride_t;
+    const T* const qm_p = base(p.q_multi);
+    const T* const do_p = base(p.grad_out);
+    const T* const ks_p = ROPE ? (const T*)a.krot + (int64_t)bh * Lp * D : base(p.k_self);
+    const int64_t ks_t = ROPE ? D : p.k_self.stride_t;
+    const T* const km_p = base(p.k_multi);
+    const T* const vs_p = base(p.v_self);
+    const T* const vm_p = base(p.v_multi);
+    const int* const keff_b = a.keff + (int64_t)b * Lp;
+    const int4* const ksum_b = reinterpret_cast<const int4*>(a.ksum) + (int64_t)b * (Lp / 32);
+
+    // ---- query-side registers (B operands) ----
+    v8 qf[2][BS::NKK], dof[BS::NKK];
+#pragma unroll
+    for (int kk = 0; kk < BS::NKK; ++kk) {
+        const int d0 = kk * 16 + hh * 8;
+        float x[8];
+        const bool ok = qin && d0 < D;
+        if (ok) load8f<T>(qs_p + (int64_t)q * qs_t, d0, x);
+        else for (int u = 0; u < 8; ++u) x[u] = 0.f;
+        qf[0][kk] = pack8<T>(x);
+        if (ok) load8f<T>(qm_p + (int64_t)q * p.q_multi.stride_t, d0, x);
+        else for (int u = 0; u < 8; ++u) x[u] = 0.f;
+        qf[1][kk] = pack8<T>(x);
+        if (ok) load8f<T>(do_p + (int64_t)q * p.grad_out.stride_t, d0, x);
+        else for (int u = 0; u < 8; ++u) x[u] = 0.f;
+        dof[kk] = pack8<T>(x);
+    }
+    const float l2 = qin ? a.lse2[(int64_t)bh * Lp + q] : INFINITY;
+    const float dl = qin ? a.delta[(int64_t)bh * Lp + q] : 0.f;
+    int cq = 0, cq_min = 0, cq_max = 0;
+    const uint8_t* mrow = nullptr;
+    if constexpr (!DENSE) {
+        cq = qin ? p.chain_id[(int64_t)b * L + q] : 0;
+        cq_min = __builtin_amdgcn_readfirstlane(wave_min_i(qin ? cq : INT32_MAX));
+        cq_max = __builtin_amdgcn_readfirstlane(wave_max_i(qin ? cq : INT32_MIN));
+    } else {
+        mrow = p.chain_mask + (int64_t)b * p.mask_stride_b + (int64_t)(qin ? q : 0) * p.mask_stride_q;
+    }
+
+    f32x16 dq[2][BS::NDB];
+#pragma unroll
+    for (int pw = 0; pw < 2; ++pw)
+#pragma unroll
+        for (int db = 0; db < BS::NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dq[pw][db][i] = 0.f;
+
+    // ---- DMA plan ----
+    const char* dsb[NJ];
+    unsigned dstr[NJ], dlds[NJ], dloff[NJ];
+    auto dma_slot = [&](int j, int& r, int& cb) {
+        const int slot = ((wave + j * W) % TS::NI) * 64 + lane;
+        r = slot / TS::NCH;
+        cb = TS::swz(r, slot % TS::NCH) * 16;
+    };
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int ins = min(wave + j * W, TOT - 1);
+        const int ten = ins / TS::NI, part = ins % TS::NI;
+        int r, cb;
+        dma_slot(j, r, cb);
+        const T* tb = ten == 0 ? ks_p : ten == 1 ? km_p : ten == 2 ? vs_p : vm_p;
+        const int64_t ts = ten == 0 ? ks_t : ten == 1 ? p.k_multi.stride_t : ten == 2 ? p.v_self.stride_t
+                                                                                       : p.v_multi.stride_t;
+        dsb[j] = (const char*)tb;
+        dstr[j] = (unsigned)(ts * (int64_t)sizeof(T));
+        dlds[j] = ten * TS::TILE + part * 1024;
+        dloff[j] = r * dstr[j] + cb;
+    }
+    const unsigned smem_base = lds_addr(smem);
+    const unsigned scid_base = lds_addr(&scid[wave][0][0]);
+    auto issue = [&](int s, int bf) {
+        const int k0 = s * kBS;
+        const unsigned lb = smem_base + bf * STAGE;
+        unsigned voff[NJ];
+        if (k0 + kBS <= L) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) voff[j] = (unsigned)k0 * dstr[j] + dloff[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                int r, cb;
+                dma_slot(j, r, cb);
+                voff[j] = (unsigned)min(k0 + r, L - 1) * dstr[j] + cb;
+            }
+        }
+        const int m0v = m0_save();
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+            if (TOT % W == 0 || wave + j * W < TOT) dma16(dsb[j], voff[j], lb + dlds[j]);
+        dma4(keff_b, (unsigned)(k0 + lane) * 4u, scid_base + bf * kBS * 4);
+        m0_restore(m0v);
+    };
+
+    // ---- operand readers ----
+    const int krow = swapped_row(ql);
+    int roff[BS::NKK];
+#pragma unroll
+    for (int kk = 0; kk < BS::NKK; ++kk) {
+        const int cch = 2 * kk + hh;
+        roff[kk] = cch < TS::NCH ? krow * TS::RB + TS::swz(krow, cch) * 16 : 0;
+    }
+    const int tg = lane >> 4, ti = lane & 15;
+    int toff[BS::NDB][2];
+#pragma unroll
+    for (int db = 0; db < BS::NDB; ++db) {
+        int e = 8 * db + 4 * (tg & 1) + (ti & 3);
+        if (8 * e >= TS::RB) e = ti & 3;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int row = 8 * (tg >> 1) + 4 * rr + (ti >> 2);
+            toff[db][rr] = row * TS::RB + TS::swz(row, e >> 1) * 16 + (e & 1) * 8;
+        }
+    }
+    v8 zero8;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) zero8[t] = (T)0.f;
+    auto rop = [&](const char* stage, int ten, int st, int kk) -> v8 {
+        if (2 * kk + hh >= TS::NCH) return zero8;
+        return *reinterpret_cast<const v8*>(stage + ten * TS::TILE + st * 32 * TS::RB + roff[kk]);
+    };
+    auto top = [&](const char* stage, int ten, int st, int cc, int db) -> v8 {
+        s4 half[2];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const char* ptr = stage + ten * TS::TILE + (st * 32 + 16 * cc) * TS::RB + toff[db][rr];
+            half[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(ptr));
+        }
+        const v8 r8 = __builtin_bit_cast(v8, __builtin_shufflevector(half[0], half[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        if constexpr (D % 32 == 0) return r8;
+        return db * 32 + (lane & 31) < D ? r8 : zero8;
+    };
+    const float c = a.c;
+    auto mma_kloop = [&](const v8* aop, const v8* bop) {
+        f32x16 acc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < BS::NKK; ++kk) acc = E::mma(aop[kk], bop[kk], acc);
+        return acc;
+    };
+
+    // One 32-key subtile; mode 0/1: pure pathway, 2: both pathways.
+    auto subtile = [&](const char* stage, const int* cid, int st, int mode, int k0) {
+        f32x16 dsv;
+        bool same[16];
+        if (mode != 2) {
+            const int pw = mode;
+            v8 ka[BS::NKK], va[BS::NKK];
+#pragma unroll
+            for (int kk = 0; kk < BS::NKK; ++kk) {
+                ka[kk] = rop(stage, pw, st, kk);
+                va[kk] = rop(stage, 2 + pw, st, kk);
+            }
+            const f32x16 sv = mma_kloop(ka, pw == 0 ? qf[0] : qf[1]);
+            const f32x16 dp = mma_kloop(va, dof);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float pv = fast_exp2(fmaf(sv[i], c, -l2));
+                dsv[i] = pv * (dp[i] - dl);
+                same[i] = pw == 0;
+            }
+        } else {
+            v8 kas[BS::NKK], kam[BS::NKK], vas[BS::NKK], vam[BS::NKK];
+#pragma unroll
+            for (int kk = 0; kk < BS::NKK; ++kk) {
+                kas[kk] = rop(stage, 0, st, kk);
+                kam[kk] = rop(stage, 1, st, kk);
+                vas[kk] = rop(stage, 2, st, kk);
+                vam[kk] = rop(stage, 3, st, kk);
+            }
+            const f32x16 ss = mma_kloop(kas, qf[0]);
+            const f32x16 sm = mma_kloop(kam, qf[1]);
+            const f32x16 dps = mma_kloop(vas, dof);
+            const f32x16 dpm = mma_kloop(vam, dof);
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                const int kl = st * 32 + 16 * cc + 8 * hh;
+                const i32x4 c0 = *reinterpret_cast<const i32x4*>(&cid[kl]);
+                const i32x4 c1 = *reinterpret_cast<const i32x4*>(&cid[kl + 4]);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int ck = t < 4 ? c0[t & 3] : c1[t & 3];
+                    const int i = 8 * cc + t;
+                    bool sm_;
+                    if constexpr (DENSE) {
+                        const int kg = k0 + kl + t;
+                        sm_ = !(kg < L && mrow[(int64_t)kg * p.mask_stride_k] != 0);
+                    } else {
+                        sm_ = ck == cq;
+                    }
+                    same[i] = sm_;
+                    const float s = sm_ ? ss[i] : sm[i];
+                    const float dp = sm_ ? dps[i] : dpm[i];
+                    const float pv = ck == kPadChain ? 0.f : fast_exp2(fmaf(s, c, -l2));
+                    dsv[i] = pv * (dp - dl);
+                }
+            }
+        }
+        // dQ^T_pw += K_pw^T dS^T
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            v8 dss, dsm;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int i = 8 * cc + t;
+                const T dv_ = (T)dsv[i];
+                dss[t] = same[i] ? dv_ : (T)0.f;
+                dsm[t] = same[i] ? (T)0.f : dv_;
+            }
+#pragma unroll
+            for (int db = 0; db < BS::NDB; ++db) {
+                if (mode != 1) dq[0][db] = E::mma(top(stage, 0, st, cc, db), dss, dq[0][db]);
+                if (mode != 0) dq[1][db] = E::mma(top(stage, 1, st, cc, db), dsm, dq[1][db]);
+            }
+        }
+    };
+
+    auto kmode = [&](int kmin, int kmax, int npad) {
+        if (npad == 32) return 3;
+        if (!DENSE && npad == 0) {
+            if (kmin == kmax && cq_min == cq_max && kmin == cq_min) return 0;
+            if (kmax < cq_min || kmin > cq_max) return 1;
+        }
+        return 2;
+    };
+
+    const int nst = (L + kBS - 1) / kBS;
+    issue(0, 0);
+    for (int s = 0; s < nst; ++s) {
+        const int bf = s & 1;
+        wait_vm<0>();
+        stage_barrier();
+        if (s + 1 < nst) issue(s + 1, bf ^ 1);
+        const char* stage = smem + bf * STAGE;
+        const int* cid = &scid[wave][bf][0];
+        const int k0 = s * kBS;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const int4 ks = ksum_b[2 * s + st];
+            const int md = kmode(__builtin_amdgcn_readfirstlane(ks.x), __builtin_amdgcn_readfirstlane(ks.y),
+                                 __builtin_amdgcn_readfirstlane(ks.z));
+            if (md == 0) subtile(stage, cid, st, 0, k0);
+            else if (md == 1) subtile(stage, cid, st, 1, k0);
+            else if (md == 2) subtile(stage, cid, st, 2, k0);
+        }
+    }
+    wait_vm<0>();
+    stage_barrier();
+
+    float* scratch = (float*)(smem + wave * 32 * 65 * 4);
+    const float scale = p.scale;
+    store_rows<T, D, true>(dq[0], scratch, p.dq_self, b, h, qw0, L, scale, ROPE, p.rope_cos, p.rope_sin);
+    store_rows<T, D, true>(dq[1], scratch, p.dq_multi, b, h, qw0, L, scale, false, nullptr, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool ROPE, bool DENSE>
+static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
+    constexpr int W = 4;
+    BwdArgs a;
+    a.p = p;
+    const int Lp = rup(p.L, kBS);
+    a.Lp = Lp;
+    a.c = p.scale * kLog2e;
+    const BwdWs ws = bwd_ws_layout(p.B, p.H, p.L, D, sizeof(T), ROPE);
+    char* w = (char*)p.workspace;
+    float* lse2 = (float*)(w + ws.lse2);
+    float* delta = (float*)(w + ws.delta);
+    int* keff = (int*)(w + ws.keff);
+    int* ksum = (int*)(w + ws.ksum);
+    int* qcid = (int*)(w + ws.qcid);
+    int* qsum = (int*)(w + ws.qsum);
+    T* qrot = (T*)(w + ws.qrot);
+    T* krot = (T*)(w + ws.krot);
+    a.lse2 = lse2;
+    a.delta = delta;
+    a.keff = keff;
+    a.ksum = ksum;
+    a.qcid = qcid;
+    a.qsum = qsum;
+    a.qrot = qrot;
+    a.krot = krot;
+    const int nchain = (p.B * (Lp / 64) + 3) / 4;
+    const int nrow = (int)(((int64_t)p.B * p.H * Lp + 255) / 256);
+    const int nrot = ROPE ? (int)((2 * (int64_t)p.B * p.H * Lp + 255) / 256) : 0;
+    hipLaunchKernelGGL((bwd_prep_kernel<T, D, ROPE, DENSE>), dim3(nchain + nrow + nrot), dim3(256), 0, stream,
+                       a, lse2, delta, keff, ksum, qcid, qsum, qrot, krot, nchain, nrow);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int nb = (p.L + 32 * W - 1) / (32 * W);
+    const unsigned grid = (unsigned)((int64_t)p.B * p.H * nb);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, DENSE>), dim3(grid), dim3(W * 64), 0, stream, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, DENSE>), dim3(grid), dim3(W * 64), 0, stream, a);
+    return hipGetLastError();
+}
+
+template <typename T, int D>
+static hipError_t dispatch_bwd_d(const mpattn_bwd_params& p, hipStream_t s) {
+    const bool rope = p.rope == MPATTN_ROPE_FUSED;
+    const bool dense = p.chain_mask != nullptr;
+    if (rope) return dense ? launch_bwd_t<T, D, true, true>(p, s) : launch_bwd_t<T, D, true, false>(p, s);
+    return dense ? launch_bwd_t<T, D, false, true>(p, s) : launch_bwd_t<T, D, false, false>(p, s);
+}
+
+template <typename T>
+static hipError_t dispatch_bwd_t(const mpattn_bwd_params& p, hipStream_t s) {
+    switch (p.D) {
+        case 16: return dispatch_bwd_d<T, 16>(p, s);
+        case 24: return dispatch_bwd_d<T, 24>(p, s);
+        case 32: return dispatch_bwd_d<T, 32>(p, s);
+        case 64: return dispatch_bwd_d<T, 64>(p, s);
+    }
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_bwd(const mpattn_bwd_params& p, hipStream_t stream) {
-    (void)p; (void)stream;
-    return hipErrorInvalidValue;
+    if (p.dtype == MPATTN_FP32 || p.sqrt_softmax) return hipErrorInvalidValue;  // not built
+    if (p.dtype == MPATTN_BF16) return dispatch_bwd_t<bf16_t>(p, stream);
+    return dispatch_bwd_t<fp16_t>(p, stream);
 }
+
 hipError_t launch_fwd32(const mpattn_fwd_params& p, hipStream_t stream) {
-    (void)p; (void)stream;
+    (void)p;
+    (void)stream;
     return hipErrorInvalidValue;
 }
+
 }  // namespace mpattn

@@ -176,4 +176,64 @@ __device__ __forceinline__ typename Elt<T>::v8 pack8(const float x[8]) {
     return r;
 }
 
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ unsigned lds_addr(const void* ptr) {
+    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
+}
+
+// global -> LDS copy (global_load_lds): lane i writes its `size` bytes at LDS
+// address M0 + i*size; the global address is sbase + voff (per lane). Issued
+// as inline asm so the compiler does not wait for it before unrelated LDS
+// reads; completion is tracked by hand with wait_vm<> and the barrier. M0 is
+// saved before a batch of copies and restored after it (m0_save/m0_restore).
+__device__ __forceinline__ int m0_save() {
+    int v;
+    asm volatile("s_mov_b32 %0, m0" : "=s"(v));
+    return v;
+}
+__device__ __forceinline__ void m0_restore(int v) { asm volatile("s_mov_b32 m0, %0" ::"s"(v)); }
+__device__ __forceinline__ void dma16(const void* sbase, unsigned voff, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :: "v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* sbase, unsigned voff, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+                 :: "v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
+
+// Wait until at most N vector-memory instructions of this wave are in flight.
+template <int N> __device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without the release fence of __syncthreads (which would
+// also drain the stages still in flight); LDS reads of this wave complete first.
+__device__ __forceinline__ void stage_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// 64-row tiles of 16-bit rows of D elements staged in LDS: rows are stored
+// densely (RB bytes each) with their 16-byte chunks XOR-swizzled by row so the
+// MFMA operand reads below hit distinct banks. The swizzle repeats every 16
+// rows (RP * NCH = 16).
+template <int D> struct TileShape {
+    static constexpr int RB = D * 2;        // row bytes
+    static constexpr int NCH = RB / 16;     // 16-byte chunks per row
+    static constexpr int TILE = 64 * RB;    // bytes per 64-row tile
+    static constexpr int NI = TILE / 1024;  // global_load_lds wave-instructions per tile
+    static constexpr bool POW2 = (NCH & (NCH - 1)) == 0;
+    static constexpr int RP = 256 / RB;     // rows per 256-byte bank window
+    static __device__ __forceinline__ int swz(int r, int c) {
+        if constexpr (POW2) return c ^ ((r / RP) & (NCH - 1));
+        return c;
+    }
+};
+
+// Row of the MFMA row-operand this lane reads for subtile row ql: bits 2 and 3
+// swapped, so accumulator slot i of lane half hh is row 16*(i/8) + 8*hh + i%8.
+__device__ __forceinline__ int swapped_row(int ql) {
+    return (ql & ~12) | ((ql & 4) << 1) | ((ql & 8) >> 1);
+}
+
 }  // namespace mpattn

@@ -186,43 +186,6 @@ template <int D> struct FwdShape {
     }
 };
 
-// LDS byte address of a __shared__ object.
-__device__ __forceinline__ unsigned lds_addr(const void* ptr) {
-    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
-}
-
-// global -> LDS copy (global_load_lds): lane i writes its `size` bytes at LDS
-// address M0 + i*size; the global address is sbase + voff (per lane). Issued
-// as inline asm so the compiler does not wait for it before unrelated LDS
-// reads; completion is tracked by hand with wait_vm<> and the barrier. M0 is
-// saved before a batch of copies and restored after it (m0_save/m0_restore).
-__device__ __forceinline__ int m0_save() {
-    int v;
-    asm volatile("s_mov_b32 %0, m0" : "=s"(v));
-    return v;
-}
-__device__ __forceinline__ void m0_restore(int v) { asm volatile("s_mov_b32 m0, %0" ::"s"(v)); }
-__device__ __forceinline__ void dma16(const void* sbase, unsigned voff, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-                 :: "v"(voff), "s"(sbase), "s"(lds) : "memory");
-}
-__device__ __forceinline__ void dma4(const void* sbase, unsigned voff, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
-                 :: "v"(voff), "s"(sbase), "s"(lds) : "memory");
-}
-
-// Wait until at most N vector-memory instructions of this wave are in flight.
-template <int N> __device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Workgroup barrier without the release fence of __syncthreads (which would
-// also drain the stages still in flight); LDS reads of this wave complete first.
-__device__ __forceinline__ void stage_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 #ifndef MPATTN_FWD_WAVES
 #define MPATTN_FWD_WAVES 4  // register budget: wavefronts per SIMD
 #endif

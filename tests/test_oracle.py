@@ -1,0 +1,346 @@
+"""Pins of the CPU oracle (runs without a GPU).
+
+Each oracle function is checked against something it does not share code
+with: closed forms and hand-computed vectors for RoPE, torch's
+``scaled_dot_product_attention`` (a library routine) on concatenated
+features for the forward, torch autograd of that construction and central
+finite differences for the backward, invariants the op must satisfy, and the
+pure-Python loop on tiny inputs. A plausible slip (a dropped term, a swapped
+pathway, a wrong sign or rotation pairing, a transposed operand) fails at
+least one of them.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import multi_chain_ids, tail_padding, two_chain_ids
+from oracle import mpattn_oracle as orc
+from oracle import torch_ref
+
+
+# ---------------------------------------------------------------------------
+# Independent restatements used as checkers
+# ---------------------------------------------------------------------------
+def rope_complex(x, positions):
+    """RoPE as complex multiplication: pair (d, d + D/2) is the complex number
+    x_d + i x_{d+D/2}, rotated by exp(i * p * theta_d), theta_d =
+    fp32(10000^(-2d/D)) and the angle one fp32 product (the reference forms
+    both in fp32)."""
+    D = x.shape[-1]
+    h = D // 2
+    theta = (10000.0 ** (-(2.0 * np.arange(h)) / D)).astype(np.float32)
+    ang = (np.asarray(positions, np.float32)[:, None] * theta[None, :]).astype(np.float64)
+    z = (x[..., :h] + 1j * x[..., h:]) * np.exp(1j * ang)
+    return np.concatenate([z.real, z.imag], axis=-1)
+
+
+def sdpa_concat(qs, ks, vs, qm, km, vm, cid, key_pad, rope, scale, requires_grad=False):
+    """The op through torch SDPA. For queries on chain c every key j gets the
+    feature k'_j = [R k_self_j, 0] if chain_j == c else [0, k_multi_j] and
+    value v_self_j / v_multi_j; the query feature is [R q_self_i, q_multi_i].
+    Then q'.k'_j is exactly the selected logit and one SDPA call per chain
+    computes the op. Returns (out, logits) as torch float64."""
+    t = lambda a: torch.as_tensor(np.asarray(a, np.float64))
+    B, H, L, D = qs.shape
+    leaves = [t(a).requires_grad_(requires_grad) for a in (qs, ks, vs, qm, km, vm)]
+    qs_t, ks_t, vs_t, qm_t, km_t, vm_t = leaves
+    if rope:
+        cos, sin = (t(a) for a in orc.rope_tables(L, D))  # tables pinned separately below
+        h = D // 2
+        rot = lambda x: torch.cat([x[..., :h] * cos - x[..., h:] * sin,
+                                   x[..., h:] * cos + x[..., :h] * sin], dim=-1)
+        qs_r, ks_r = rot(qs_t), rot(ks_t)
+    else:
+        qs_r, ks_r = qs_t, ks_t
+    out = torch.zeros(B, H, L, D, dtype=torch.float64)
+    logits = torch.zeros(B, H, L, L, dtype=torch.float64)
+    zero = torch.zeros(H, L, D, dtype=torch.float64)
+    for b in range(B):
+        valid = ~torch.as_tensor(np.asarray(key_pad[b], bool))
+        for c in np.unique(cid[b]):
+            qi = torch.as_tensor(np.nonzero(cid[b] == c)[0])
+            same = torch.as_tensor(cid[b] == c)[None, :, None]
+            kfeat = torch.cat([torch.where(same, ks_r[b], zero), torch.where(same, zero, km_t[b])], -1)
+            vfeat = torch.where(same, vs_t[b], vm_t[b])
+            qfeat = torch.cat([qs_r[b][:, qi], qm_t[b][:, qi]], -1)
+            mask = valid[None, None, :].expand(H, len(qi), L)
+            o = F.scaled_dot_product_attention(qfeat, kfeat, vfeat, attn_mask=mask, scale=scale)
+            out[b][:, qi] = o
+            logits[b][:, qi] = scale * qfeat @ kfeat.transpose(-1, -2)
+    return out, logits, leaves
+
+
+def rand_inputs(rng, B, H, L, D, sigma=None):
+    sigma = D ** -0.5 if sigma is None else sigma
+    return [rng.standard_normal((B, H, L, D)) * sigma for _ in range(6)]
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+def test_rope_half_split_known_vector():
+    """D = 4, position 1, x = e_0: half-split pairs (0, 2), so R x =
+    [cos 1, 0, sin 1, 0] (an interleaved layout would give [cos 1, sin 1, 0, 0])."""
+    cos, sin = orc.rope_tables(2, 4)
+    x = np.zeros((2, 4))
+    x[1, 0] = 1.0
+    y = orc.apply_rope(x, cos, sin)
+    np.testing.assert_allclose(y[1], [np.cos(1.0), 0.0, np.sin(1.0), 0.0], atol=1e-15)
+    # second frequency: theta_1 = 10000^(-2/4) = 1/100
+    x[1] = [0, 1, 0, 0]
+    y = orc.apply_rope(x, cos, sin)
+    a = float(np.float32(1.0) * np.float32(0.01))
+    np.testing.assert_allclose(y[1], [0.0, np.cos(a), 0.0, np.sin(a)], atol=1e-15)
+
+
+@pytest.mark.parametrize("D", [16, 24, 32, 64])
+def test_rope_matches_complex_rotation(D):
+    rng = np.random.default_rng(D)
+    L = 300
+    x = rng.standard_normal((3, L, D))
+    cos, sin = orc.rope_tables(L, D)
+    np.testing.assert_allclose(orc.apply_rope(x, cos, sin), rope_complex(x, np.arange(L)),
+                               atol=1e-12)
+
+
+def test_rope_identity_norm_and_transpose():
+    rng = np.random.default_rng(1)
+    L, D = 64, 32
+    x = rng.standard_normal((2, L, D))
+    g = rng.standard_normal((2, L, D))
+    cos, sin = orc.rope_tables(L, D)
+    y = orc.apply_rope(x, cos, sin)
+    np.testing.assert_allclose(y[:, 0], x[:, 0], atol=0)  # position 0: identity
+    np.testing.assert_allclose(np.linalg.norm(y, axis=-1), np.linalg.norm(x, axis=-1), rtol=1e-12)
+    # <R x, g> == <x, R^T g>
+    np.testing.assert_allclose((y * g).sum(), (x * orc.apply_rope_transpose(g, cos, sin)).sum(),
+                               rtol=1e-12)
+    np.testing.assert_allclose(orc.apply_rope_transpose(y, cos, sin), x, atol=1e-12)
+
+
+def test_rope_relative_position():
+    """<R_i q, R_j k> = <q, R_{j-i} k>: only the offset matters (up to the
+    fp32 rounding of the angle, ~1e-5 rad at these positions)."""
+    rng = np.random.default_rng(2)
+    L, D = 200, 32
+    cos, sin = orc.rope_tables(L, D)
+    q, k = rng.standard_normal(D), rng.standard_normal(D)
+    for i, j in [(0, 5), (17, 60), (100, 199), (42, 42)]:
+        Q = np.zeros((L, D)); Q[i] = q
+        K = np.zeros((L, D)); K[j] = k
+        lhs = orc.apply_rope(Q, cos, sin)[i] @ orc.apply_rope(K, cos, sin)[j]
+        K2 = np.zeros((L, D)); K2[j - i] = k
+        rhs = q @ orc.apply_rope(K2, cos, sin)[j - i]
+        assert abs(lhs - rhs) < 1e-4 * np.linalg.norm(q) * np.linalg.norm(k)
+
+
+# ---------------------------------------------------------------------------
+# Forward
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("nchains,L,D", [(1, 33, 16), (2, 64, 32), (3, 57, 24), (4, 40, 64)])
+def test_forward_vs_sdpa_concat(rope, nchains, L, D):
+    rng = np.random.default_rng(100 + L + D + nchains)
+    B, H = 2, 3
+    xs = rand_inputs(rng, B, H, L, D, sigma=0.7)
+    cid = multi_chain_ids(rng, B, L, nchains) if nchains != 2 else two_chain_ids(rng, B, L)
+    if nchains == 3:  # non-contiguous chains too
+        cid = rng.integers(0, 3, size=(B, L)).astype(np.int32)
+    kp = tail_padding(rng, B, L, 0.2)
+    scale = D ** -0.5
+    out, lse = orc.mpattn_forward(*xs, chain_ids=cid, key_pad=kp, rope=rope, scale=scale)
+    ref, logits, _ = sdpa_concat(*xs, cid, kp, rope, scale)
+    np.testing.assert_allclose(out, ref.numpy(), atol=1e-12, rtol=1e-10)
+    # LSE: logsumexp over valid keys of the SDPA construction's logits
+    lg = logits.numpy()
+    lg = np.where(kp[:, None, None, :], -np.inf, lg)
+    np.testing.assert_allclose(lse, np.logaddexp.reduce(lg, axis=-1), atol=1e-12)
+
+
+def test_forward_single_chain_is_sdpa_with_rope():
+    rng = np.random.default_rng(5)
+    B, H, L, D = 2, 2, 50, 32
+    xs = rand_inputs(rng, B, H, L, D)
+    cid = np.zeros((B, L), np.int32)
+    kp = tail_padding(rng, B, L, 0.2)
+    out, _ = orc.mpattn_forward(*xs, chain_ids=cid, key_pad=kp, rope=True, scale=D ** -0.5)
+    pos = np.arange(L)
+    qr = torch.as_tensor(rope_complex(xs[0], pos))
+    kr = torch.as_tensor(rope_complex(xs[1], pos))
+    mask = torch.as_tensor(~kp)[:, None, None, :]
+    ref = F.scaled_dot_product_attention(qr, kr, torch.as_tensor(xs[2]), attn_mask=mask)
+    np.testing.assert_allclose(out, ref.numpy(), atol=1e-10)
+
+
+def test_forward_all_cross_mask_is_sdpa_multi():
+    """A dense mask that is True everywhere selects the multimer pathway only."""
+    rng = np.random.default_rng(6)
+    B, H, L, D = 2, 2, 45, 16
+    xs = rand_inputs(rng, B, H, L, D)
+    cm = np.ones((B, L, L), bool)
+    out, _ = orc.mpattn_forward(*xs, chain_mask=cm, rope=True, scale=0.3)
+    t = [torch.as_tensor(a) for a in xs]
+    ref = F.scaled_dot_product_attention(t[3], t[4], t[5], scale=0.3)
+    np.testing.assert_allclose(out, ref.numpy(), atol=1e-12)
+
+
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("nchains", [1, 2, 3])
+def test_forward_vs_python_loops(rope, nchains):
+    rng = np.random.default_rng(7 + nchains)
+    B, H, L, D = 2, 1, 37, 8
+    xs = rand_inputs(rng, B, H, L, D, sigma=0.8)
+    cid = rng.integers(0, nchains, size=(B, L)).astype(np.int32)
+    kp = tail_padding(rng, B, L, 0.3)
+    out, _ = orc.mpattn_forward(*xs, chain_ids=cid, key_pad=kp, rope=rope, scale=0.4)
+    loops = orc.mpattn_forward_loops(*[a.tolist() for a in xs], cid.tolist(), kp.tolist(),
+                                     rope=rope, scale=0.4)
+    np.testing.assert_allclose(out, loops, atol=1e-12)
+
+
+def test_forward_invariants():
+    rng = np.random.default_rng(8)
+    B, H, L, D = 2, 2, 40, 16
+    xs = rand_inputs(rng, B, H, L, D)
+    cid = rng.integers(0, 3, size=(B, L)).astype(np.int32)
+    kp = tail_padding(rng, B, L, 0.2)
+    kw = dict(key_pad=kp, rope=True, scale=0.25)
+    out, _ = orc.mpattn_forward(*xs, chain_ids=cid, **kw)
+    # relabelling chains changes nothing
+    perm = np.array([7, -3, 11], np.int32)
+    out2, _ = orc.mpattn_forward(*xs, chain_ids=perm[cid], **kw)
+    np.testing.assert_allclose(out, out2, atol=0)
+    # appended padded keys change nothing for the original queries
+    ext = [np.concatenate([a, rng.standard_normal((B, H, 5, D))], axis=2) for a in xs]
+    cid_e = np.concatenate([cid, rng.integers(0, 3, size=(B, 5)).astype(np.int32)], axis=1)
+    kp_e = np.concatenate([kp, np.ones((B, 5), bool)], axis=1)
+    out_e, _ = orc.mpattn_forward(*ext, chain_ids=cid_e, key_pad=kp_e, rope=True, scale=0.25)
+    np.testing.assert_allclose(out_e[:, :, :L], out, atol=1e-14)
+    # constant V: every row of a valid sample is that constant
+    ones = np.ones((B, H, L, D))
+    o1, _ = orc.mpattn_forward(xs[0], xs[1], ones, xs[3], xs[4], ones, chain_ids=cid, **kw)
+    np.testing.assert_allclose(o1, 1.0, atol=1e-14)
+    # zero queries: uniform weights -> mean over valid keys of the selected V
+    z = np.zeros_like(xs[0])
+    o0, _ = orc.mpattn_forward(z, xs[1], xs[2], z, xs[4], xs[5], chain_ids=cid, **kw)
+    same = cid[:, :, None] == cid[:, None, :]
+    w = (~kp)[:, None, :] / (~kp).sum(-1)[:, None, None]
+    ref = np.einsum("bij,bhjd->bhid", np.where(same, w, 0), xs[2]) + \
+        np.einsum("bij,bhjd->bhid", np.where(same, 0, w), xs[5])
+    np.testing.assert_allclose(o0, ref, atol=1e-14)
+    # L = 1: the only key is the query's own (same chain) -> v_self
+    x1 = [a[:, :, :1] for a in xs]
+    o_1, _ = orc.mpattn_forward(*x1, chain_ids=cid[:, :1], rope=True, scale=0.25)
+    np.testing.assert_allclose(o_1, xs[2][:, :, :1], atol=0)
+
+
+def test_forward_all_padded_sample():
+    rng = np.random.default_rng(9)
+    B, H, L, D = 2, 2, 20, 16
+    xs = rand_inputs(rng, B, H, L, D)
+    cid = two_chain_ids(rng, B, L)
+    kp = np.zeros((B, L), bool)
+    kp[1] = True
+    out, lse = orc.mpattn_forward(*xs, chain_ids=cid, key_pad=kp, rope=True, scale=0.25)
+    assert np.all(out[1] == 0) and np.all(np.isneginf(lse[1]))
+    assert np.all(np.isfinite(out[0])) and np.all(np.isfinite(lse[0]))
+
+
+def test_forward_sqrt_softmax_closed_form():
+    """sqrt_softmax: O = sum_j sqrt(P_ij) V_sel, with P the softmax of the
+    concatenated-feature logits over valid keys."""
+    rng = np.random.default_rng(10)
+    B, H, L, D = 1, 2, 30, 16
+    xs = rand_inputs(rng, B, H, L, D)
+    cid = two_chain_ids(rng, B, L)
+    kp = tail_padding(rng, B, L, 0.2)
+    out, _ = orc.mpattn_forward(*xs, chain_ids=cid, key_pad=kp, rope=True, scale=0.25,
+                                sqrt_softmax=True)
+    _, logits, _ = sdpa_concat(*xs, cid, kp, True, 0.25)
+    lg = np.where(kp[:, None, None, :], -np.inf, logits.numpy())
+    P = np.exp(lg - np.logaddexp.reduce(lg, axis=-1, keepdims=True))
+    same = (cid[:, :, None] == cid[:, None, :])[:, None]
+    ref = np.einsum("bhij,bhjd->bhid", np.where(same, np.sqrt(P), 0), xs[2]) + \
+        np.einsum("bhij,bhjd->bhid", np.where(same, 0, np.sqrt(P)), xs[5])
+    np.testing.assert_allclose(out, ref, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# Backward
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rope", [False, True])
+def test_backward_vs_autograd_of_sdpa_concat(rope):
+    rng = np.random.default_rng(20 + rope)
+    B, H, L, D = 2, 2, 36, 16
+    xs = rand_inputs(rng, B, H, L, D, sigma=0.6)
+    cid = rng.integers(0, 3, size=(B, L)).astype(np.int32)
+    kp = tail_padding(rng, B, L, 0.2)
+    go = rng.standard_normal((B, H, L, D))
+    grads = orc.mpattn_backward(*xs, go, chain_ids=cid, key_pad=kp, rope=rope, scale=0.3)
+    out, _, leaves = sdpa_concat(*xs, cid, kp, rope, 0.3, requires_grad=True)
+    (out * torch.as_tensor(go)).sum().backward()
+    for g, leaf in zip(grads, leaves):
+        np.testing.assert_allclose(g, leaf.grad.numpy(), atol=1e-11)
+
+
+@pytest.mark.parametrize("sqrt_softmax", [False, True])
+def test_backward_finite_differences(sqrt_softmax):
+    rng = np.random.default_rng(30 + sqrt_softmax)
+    B, H, L, D = 1, 2, 14, 8
+    xs = rand_inputs(rng, B, H, L, D, sigma=0.7)
+    cid = two_chain_ids(rng, B, L)
+    kp = np.zeros((B, L), bool)
+    kp[0, -3:] = True
+    go = rng.standard_normal((B, H, L, D))
+    kw = dict(chain_ids=cid, key_pad=kp, rope=True, scale=0.35, sqrt_softmax=sqrt_softmax)
+    grads = orc.mpattn_backward(*xs, go, **kw)
+
+    def f(args):
+        return float((orc.mpattn_forward(*args, **kw)[0] * go).sum())
+
+    eps = 1e-6
+    for i in range(6):
+        for trial in range(2):
+            d = rng.standard_normal(xs[i].shape)
+            plus = [a.copy() for a in xs]
+            minus = [a.copy() for a in xs]
+            plus[i] += eps * d
+            minus[i] -= eps * d
+            fd = (f(plus) - f(minus)) / (2 * eps)
+            an = float((grads[i] * d).sum())
+            assert abs(fd - an) <= 1e-6 * max(1.0, abs(an)), (i, trial, fd, an)
+
+
+def test_backward_dense_mask_equals_chain_ids():
+    rng = np.random.default_rng(40)
+    B, H, L, D = 2, 2, 30, 16
+    xs = rand_inputs(rng, B, H, L, D)
+    cid = rng.integers(0, 2, size=(B, L)).astype(np.int32)
+    go = rng.standard_normal((B, H, L, D))
+    a = orc.mpattn_backward(*xs, go, chain_ids=cid, rope=False, scale=1.0)
+    b = orc.mpattn_backward(*xs, go, chain_mask=cid[:, :, None] != cid[:, None, :], rope=False,
+                            scale=1.0)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+
+
+# ---------------------------------------------------------------------------
+# torch restatement used at the benchmark shape
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dense", [False, True])
+def test_torch_ref_matches_oracle(dense):
+    rng = np.random.default_rng(50 + dense)
+    B, H, L, D = 3, 2, 70, 32
+    xs = rand_inputs(rng, B, H, L, D)
+    cid = two_chain_ids(rng, B, L)
+    kp = tail_padding(rng, B, L, 0.2)
+    kp[2] = True
+    out, lse = orc.mpattn_forward(*xs, chain_ids=cid, key_pad=kp, rope=True, scale=D ** -0.5)
+    t = [torch.as_tensor(a) for a in xs]
+    sel = dict(chain_mask=torch.as_tensor(cid[:, :, None] != cid[:, None, :])) if dense else \
+        dict(chain_ids=torch.as_tensor(cid))
+    o2, l2 = torch_ref.forward(*t, key_pad=torch.as_tensor(kp), rope=True, scale=D ** -0.5,
+                               dtype=torch.float64, chunk=2, **sel)
+    np.testing.assert_allclose(o2.numpy(), out, atol=1e-12)
+    np.testing.assert_allclose(l2.numpy(), lse, atol=1e-12)
