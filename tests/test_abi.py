@@ -1,0 +1,156 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/mpattn.h declares with the layout the ctypes binding assumes, and
+rejects invalid or unsupported requests before anything is enqueued."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from mint_plus_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "mpattn.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(mpattn_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libmpattn.so is not built (run __graft_entry__.build())")
+    return _lib.load_library()
+
+
+def test_exports_every_header_function(lib):
+    names = header_functions()
+    assert "mpattn_fwd" in names and "mpattn_bwd" in names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in mpattn.h but not exported"
+        assert n in _lib.EXPORTS, f"{n} has no ctypes signature in _lib.EXPORTS"
+    assert set(_lib.EXPORTS) == set(names)
+
+
+def test_version_and_strings(lib):
+    assert lib.mpattn_version() == 1
+    assert lib.mpattn_strerror(0) == b"success"
+    assert lib.mpattn_strerror(-2) == b"unsupported configuration"
+    assert lib.mpattn_strerror(-99) == b"unknown error"
+
+
+def test_struct_layout_matches_header():
+    """Field offsets of the ctypes mirrors follow the C declaration order with
+    natural alignment (x86-64 SysV, the layout hipcc's host pass uses)."""
+    assert ctypes.sizeof(_lib.Tensor4) == 32
+    f = _lib.FwdParams
+    assert f.out.offset == 6 * 32 and f.lse.offset == 7 * 32
+    assert f.B.offset == f.rope_sin.offset + 8
+    assert f.workspace.offset % 8 == 0
+    b = _lib.BwdParams
+    assert b.grad_out.offset == 7 * 32 and b.lse.offset == 8 * 32
+    assert b.dv_multi.offset == 8 * 32 + 8 + 5 * 32
+
+
+def test_workspace_sizes(lib):
+    assert lib.mpattn_fwd_workspace_size(0, 1, 1, 32, 0, 1) == -1
+    assert lib.mpattn_bwd_workspace_size(1, 0, 1, 32) == -1
+    a = lib.mpattn_fwd_workspace_size(16, 20, 1024, 32, 0, 1)
+    b = lib.mpattn_fwd_workspace_size(16, 20, 1024, 32, 0, 0)
+    assert a > b > 0  # fused RoPE stages rotated K_self in the workspace
+    assert a >= 16 * 20 * 1024 * 32 * 2
+    w = lib.mpattn_bwd_workspace_size(8, 20, 1024, 32)
+    assert w >= 2 * 8 * 20 * 1024 * 4  # LSE and Delta rows at least
+
+
+def _fake(ptr=1 << 20):
+    return _lib.Tensor4(ptr, 40960, 2048, 32)
+
+
+def _fwd_params(**over):
+    p = _lib.FwdParams()
+    for n in ("q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi", "out"):
+        setattr(p, n, _fake())
+    p.chain_id = 1 << 21
+    p.rope_cos = p.rope_sin = 1 << 22
+    p.B, p.H, p.L, p.D = 2, 20, 64, 32
+    p.dtype, p.rope, p.scale = _lib.MPATTN_BF16, _lib.MPATTN_ROPE_FUSED, 32 ** -0.5
+    p.workspace, p.workspace_bytes = 1 << 24, 1 << 30
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+# Each case fails validation, so nothing reaches the HIP runtime.
+FWD_CASES = [
+    (dict(D=48), _lib.MPATTN_ERR_UNSUPPORTED, "head dim"),
+    (dict(L=0), _lib.MPATTN_ERR_INVALID, "must be >= 1"),
+    (dict(dtype=7), _lib.MPATTN_ERR_INVALID, "dtype"),
+    (dict(rope=5), _lib.MPATTN_ERR_INVALID, "rope"),
+    (dict(scale=0.0), _lib.MPATTN_ERR_INVALID, "scale"),
+    (dict(scale=float("nan")), _lib.MPATTN_ERR_INVALID, "scale"),
+    (dict(chain_mask=1 << 23), _lib.MPATTN_ERR_INVALID, "exactly one"),
+    (dict(chain_id=None), _lib.MPATTN_ERR_INVALID, "exactly one"),
+    (dict(rope_cos=None), _lib.MPATTN_ERR_INVALID, "rope tables"),
+    (dict(dropout_p=0.1), _lib.MPATTN_ERR_UNSUPPORTED, "dropout"),
+    (dict(q_self=_lib.Tensor4(None, 0, 0, 32)), _lib.MPATTN_ERR_INVALID, "null"),
+    (dict(k_self=_lib.Tensor4((1 << 20) + 8, 40960, 2048, 32)), _lib.MPATTN_ERR_UNSUPPORTED, "aligned"),
+    (dict(v_multi=_lib.Tensor4(1 << 20, 40960, 2048, 36)), _lib.MPATTN_ERR_UNSUPPORTED, "multiples"),
+    (dict(workspace_bytes=16), _lib.MPATTN_ERR_INVALID, "workspace"),
+    (dict(workspace=(1 << 24) + 16), _lib.MPATTN_ERR_INVALID, "workspace"),
+]
+
+
+@pytest.mark.parametrize("over,code,msg", FWD_CASES)
+def test_fwd_validation(lib, over, code, msg):
+    p = _fwd_params(**over)
+    rc = lib.mpattn_fwd(ctypes.byref(p), None)
+    assert rc == code
+    assert msg in lib.mpattn_last_error().decode()
+
+
+def test_null_params(lib):
+    assert lib.mpattn_fwd(None, None) == _lib.MPATTN_ERR_INVALID
+    assert lib.mpattn_bwd(None, None) == _lib.MPATTN_ERR_INVALID
+
+
+def test_bwd_validation(lib):
+    p = _lib.BwdParams()
+    for n in ("q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi", "out", "grad_out",
+              "dq_self", "dk_self", "dv_self", "dq_multi", "dk_multi", "dv_multi"):
+        setattr(p, n, _fake())
+    p.chain_id = 1 << 21
+    p.B, p.H, p.L, p.D = 2, 20, 64, 32
+    p.dtype, p.rope, p.scale = _lib.MPATTN_BF16, _lib.MPATTN_ROPE_NONE, 1.0
+    p.workspace = 1 << 24
+    # lse missing
+    assert lib.mpattn_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
+    assert "lse" in lib.mpattn_last_error().decode()
+    p.lse = 1 << 25
+    p.D = 40
+    assert lib.mpattn_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_UNSUPPORTED
+
+
+def test_python_api_rejects_cpu_tensors():
+    """No CPU fallback: host tensors are refused, never computed."""
+    import mint_plus_amd as m
+    x = torch.zeros(1, 2, 16, 32, dtype=torch.bfloat16)
+    cid = torch.zeros(1, 16, dtype=torch.int32)
+    with pytest.raises((RuntimeError, AssertionError, ValueError)):
+        m.fused_multi_pathway_attention(x, x, x, x, x, x, None, chain_ids=cid, training=False)
+
+
+def test_python_api_shape_asserts():
+    """Shape mismatches raise AssertionError as in the reference wrapper."""
+    import mint_plus_amd as m
+    x = torch.zeros(1, 2, 16, 32, dtype=torch.bfloat16)
+    y = torch.zeros(1, 2, 17, 32, dtype=torch.bfloat16)
+    mask = torch.zeros(1, 16, 16, dtype=torch.bool)
+    with pytest.raises(AssertionError):
+        m.fused_multi_pathway_attention(x, y, x, x, x, x, mask, training=False)
+    with pytest.raises(AssertionError):
+        m.fused_multi_pathway_attention(x, x, x, x, x, x, mask[:, :8], training=False)
