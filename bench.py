@@ -49,12 +49,22 @@ def make_workload(device, seed=SEED):
     return xs, cid.to(device), pad.to(device)
 
 
-def flops_fwd():
-    return 4.0 * B * H * L * L * D
+def flops_fwd(b=B):
+    return 4.0 * b * H * L * L * D
 
 
-def bytes_fwd():
-    return 7.0 * B * H * L * D * 2 + B * L * 5
+def flops_bwd(b=B):
+    """dV, dP, dQ, dK: four L x L x D contractions per (b, h); recompute excluded."""
+    return 8.0 * b * H * L * L * D
+
+
+def bytes_fwd(b=B):
+    return 7.0 * b * H * L * D * 2 + b * L * 5
+
+
+def bytes_bwd(b=B):
+    """6 inputs + O + dO read, 6 gradients written (bf16), LSE read, chain ids."""
+    return 14.0 * b * H * L * D * 2 + b * H * L * 4 + b * L * 5
 
 
 def cpu_baseline(budget_s=20.0):
@@ -92,6 +102,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mode", choices=("fwd", "fwdbwd"), default="fwd",
+                    help="fwd: the headline forward (B=16); fwdbwd: forward + backward at the "
+                         "training shape (B=8, dO ~ N(0, 1))")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="time a plain device copy of MIB MiB instead (HBM counter calibration)")
     args = ap.parse_args()
@@ -121,6 +134,8 @@ def main():
         ms = e0.elapsed_time(e1) / args.steps
         print(json.dumps({"copy_bytes": n, "ms": ms, "GB/s": 2 * n / ms / 1e6}), flush=True)
         return
+    if args.mode == "fwdbwd":
+        return bench_fwdbwd(args, dev)
     xs, cid, pad = make_workload(dev)
     out = torch.empty_like(xs[0])
 
@@ -172,11 +187,92 @@ def main():
         "hbm_gbs_algorithmic": round(bytes_fwd() / (med * 1e-3) / 1e9, 1),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic("fwd_150m")},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(res), flush=True)
+
+
+def measured_traffic(key):
+    """HBM bytes per call from the committed rocprofv3 --pmc summary
+    (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE per dispatch, scaled by
+    the factors a plain copy of known size gives), or None if absent."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)[key]
+    except (OSError, KeyError, ValueError):
+        return None
+    return int(rec["bytes_per_call"])
+
+
+def timed(step, steps, warmup, stream):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    return wall, per
+
+
+def bench_fwdbwd(args, dev):
+    """Forward (saving LSE) + backward at configs[3]: B=8, dO ~ N(0, 1)."""
+    from mint_plus_amd import _lib
+    b8 = 8
+    xs, cid, pad = make_workload(dev)
+    xs = [x[:b8].contiguous() for x in xs]
+    cid, pad = cid[:b8].contiguous(), pad[:b8].contiguous()
+    g = torch.Generator(device="cpu").manual_seed(SEED + 1)
+    go = torch.randn(b8, H, L, D, generator=g).to(torch.bfloat16).to(dev)
+    sel = dict(chain_ids=cid, key_padding_mask=pad, rope=True, scale=D ** -0.5)
+    out = torch.empty_like(xs[0])
+
+    def step():
+        _, lse = _lib.mpattn_fwd(*xs, need_lse=True, out=out, **sel)
+        _lib.mpattn_bwd(*xs, out, lse, go, **sel)
+
+    stream = torch.cuda.current_stream(dev)
+    wall, per = timed(step, args.steps, args.warmup, stream)
+    med = statistics.median(per)
+    mean_ms = sum(per) / len(per)
+    fl = flops_fwd(b8) + flops_bwd(b8)
+    tflops = fl / (med * 1e-3) / 1e12
+    achieved = fl / (mean_ms * 1e-3) / 1e12
+    res = {
+        "metric": "multi-pathway attn fwd+bwd TFLOP/s (150M training shape, bf16)",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)/sqrt(32) projections, 2 chains, 0-10% pad tail, "
+                "dO ~ N(0,1))",
+        "config": {"workload": "multi-pathway attention forward+backward, frozen-150M "
+                               "training shape", "B": b8, "H": H, "L": L, "D": D,
+                   "rope": "fused", "chains": 2},
+        "kernel_ms": {"median": round(med, 5), "p10": round(per[len(per) // 10], 5),
+                      "p90": round(per[(9 * len(per)) // 10], 5), "mean": round(mean_ms, 5)},
+        "flops_per_step": fl,
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic("fwdbwd_150m_b8")},
+        "cpu_baseline": None,
+    }
     print(json.dumps(res), flush=True)
 
 
