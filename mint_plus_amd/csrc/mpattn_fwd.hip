@@ -166,34 +166,24 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p
 // ---------------------------------------------------------------------------
 // Main kernel.
 // ---------------------------------------------------------------------------
-template <int D> struct FwdShape {
+template <int D> struct FwdShape : TileShape<D> {
     static constexpr int DP = D <= 16 ? 16 : (D <= 32 ? 32 : 64);  // MFMA K for QK^T
     static constexpr int NKK = DP / 16;                              // QK MFMAs / subtile
     static constexpr int NDB = DP <= 32 ? 1 : 2;                     // 32-row blocks of O^T
-    static constexpr bool SUM_MFMA = D < 32;                         // ones rows give the sum
-    static constexpr int ISUM = 4 * (D / 8);                         // accumulator slot of row D
-    static constexpr int RB = D * 2;                                 // LDS row bytes
-    static constexpr int NCH = RB / 16;                              // 16-byte chunks per row
-    static constexpr int TILE = kBN * RB;                            // bytes per tensor tile
-    static constexpr int STAGE = 4 * TILE;
-    static constexpr int NI = TILE / 1024;                           // DMA wave-instr per tile
-    static constexpr bool POW2 = (NCH & (NCH - 1)) == 0;
-    static constexpr int ROWS_PER_256 = 256 / RB;
-    // physical 16-byte chunk of logical chunk c in row r
-    static __device__ __forceinline__ int swz(int r, int c) {
-        if constexpr (POW2) return c ^ ((r / ROWS_PER_256) & (NCH - 1));
-        return c;
-    }
+    static constexpr int STAGE = 4 * TileShape<D>::TILE;             // K_s, K_m, V_s, V_m
+    static constexpr int W = D == 64 ? 4 : 8;                        // wavefronts per workgroup
 };
 
 #ifndef MPATTN_FWD_WAVES
 #define MPATTN_FWD_WAVES 4  // register budget: wavefronts per SIMD
 #endif
-#ifndef MPATTN_FWD_NBUF32
-#define MPATTN_FWD_NBUF32 2  // LDS stages in flight for D <= 32
-#endif
 
-template <typename T, int D, int W, int NBUF, bool ROPE, bool DENSE>
+// Row sums above this bound (or not finite) send a stage through the fix-up
+// path, which moves the row's reference max. 2^64 keeps every partial sum and
+// accumulator far from fp32 overflow.
+constexpr float kSumHi = 18446744073709551616.0f;
+
+template <typename T, int D, int W, bool ROPE, bool DENSE>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(MPATTN_FWD_WAVES)))
 void fwd_kernel(const FwdArgs args) {
     using S = FwdShape<D>;
@@ -201,10 +191,11 @@ void fwd_kernel(const FwdArgs args) {
     typedef typename E::v8 v8;
     typedef typename E::v2 v2;
     typedef short s4 __attribute__((ext_vector_type(4)));
-    typedef short s8 __attribute__((ext_vector_type(8)));
-    constexpr int TOT = 4 * S::NI;  // DMA instructions per stage
-    static_assert(TOT % W == 0, "stage DMA must split evenly over waves");
-    constexpr int IPW = TOT / W + 1;  // per wave per stage, incl. the chain ids
+    constexpr int NBUF = 2;
+    constexpr int TOT = 4 * S::NI;              // DMA wave-instructions per full stage
+    constexpr int NJ = (TOT + W - 1) / W;       // per wavefront (the last may be idle)
+    // With fused RoPE the logit factor scale*log2(e) is folded into Q.
+    constexpr bool FOLDED = ROPE;
     const mpattn_fwd_params& p = args.p;
 
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * S::STAGE];
@@ -218,7 +209,8 @@ void fwd_kernel(const FwdArgs args) {
     const int g = xcd_remap(blockIdx.x, gridDim.x);
     const int qb = g % nqb, bh = g / nqb;
     const int b = bh / H, h = bh % H;
-    const int q = qb * 32 * W + wave * 32 + ql;
+    const int qw0 = qb * 32 * W;  // first query of the workgroup
+    const int q = qw0 + wave * 32 + ql;
     const bool qvalid = q < L;
 
     auto base = [&](const mpattn_tensor& t) {
@@ -235,18 +227,19 @@ void fwd_kernel(const FwdArgs args) {
     const int* const keff_b = args.keff + (int64_t)b * Lp;
     const int4* const ksum_b = reinterpret_cast<const int4*>(args.ksum) + (int64_t)b * (Lp / 32);
 
-    // ---- DMA plan: this wave's TOT/W tile copies per stage ----
-    // Copy j covers 16-byte slots [64*part, 64*part + 64) of tensor `ten`;
-    // lane -> (row r, logical chunk c) with the physical slot swizzled.
-    constexpr int NJ = TOT / W;
-    const char* dsb[NJ];     // (b, h) base of the source tensor (uniform)
-    unsigned dstr[NJ];       // row stride in bytes (uniform)
-    unsigned dlds[NJ];       // LDS offset inside a stage (uniform)
-    unsigned dloff[NJ];      // per-lane byte offset of (r, c) relative to row 0
-    int drow[NJ], dcol[NJ];  // per-lane row and chunk byte offset
+    // ---- DMA plan: copy j of this wavefront covers 16-byte slots
+    // [64*part, 64*part + 64) of tile `ten` (0 K_self, 1 K_multi, 2 V_self,
+    // 3 V_multi); lane -> (row r, logical chunk c), physical slot swizzled.
+    const char* dsb[NJ];  // (b, h) base of the source tensor (uniform)
+    unsigned dstr[NJ];    // row stride in bytes (uniform)
+    unsigned dlds[NJ];    // LDS offset inside a stage (uniform)
+    unsigned dloff[NJ];   // per-lane byte offset of (r, c) relative to row 0
+    int drow[NJ], dcol[NJ];
+    int dten[NJ];         // tile index, 4 for an idle copy (uniform)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        const int ins = wave + j * W;
+        const int ins0 = wave + j * W;
+        const int ins = ins0 < TOT ? ins0 : TOT - 1;
         const int ten = ins / S::NI, part = ins % S::NI;
         const int slot = part * 64 + lane;
         const int r = slot / S::NCH, pc = slot % S::NCH;
@@ -259,12 +252,13 @@ void fwd_kernel(const FwdArgs args) {
         drow[j] = r;
         dcol[j] = cb;
         dloff[j] = r * dstr[j] + cb;
+        dten[j] = ins0 < TOT ? ten : 4;
     }
     const unsigned smem_base = lds_addr(smem);
     const unsigned scid_base = lds_addr(&scid[wave][0][0]);
 
-    // ---- issue the DMA of stage s into buffer bf ----
-    auto issue = [&](int s, int bf) {
+    // ---- copy stage s into buffer bf: only the pathways the workgroup needs ----
+    auto issue = [&](int s, int bf, int tiles) {
         const int k0 = s * kBN;
         const unsigned lb = smem_base + bf * S::STAGE;
         unsigned voff[NJ];
@@ -277,7 +271,8 @@ void fwd_kernel(const FwdArgs args) {
         }
         const int m0v = m0_save();
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) dma16(dsb[j], voff[j], lb + dlds[j]);
+        for (int j = 0; j < NJ; ++j)
+            if ((tiles >> dten[j]) & 1) dma16(dsb[j], voff[j], lb + dlds[j]);
         dma4(keff_b, (unsigned)(k0 + lane) * 4u, scid_base + bf * kBN * 4);
         m0_restore(m0v);
     };
@@ -301,30 +296,38 @@ void fwd_kernel(const FwdArgs args) {
             qf[pw][kk] = pack8<T>(x);
         }
     }
-    int cq = 0, cq_min = 0, cq_max = 0;
+    // Query chain ranges of this wavefront and of the whole workgroup.
+    int cq = 0, cq_min = 0, cq_max = 0, wq_min = 0, wq_max = 0;
     if constexpr (!DENSE) {
         cq = qvalid ? p.chain_id[(int64_t)b * L + q] : 0;
         cq_min = __builtin_amdgcn_readfirstlane(wave_min_i(qvalid ? cq : INT32_MAX));
         cq_max = __builtin_amdgcn_readfirstlane(wave_max_i(qvalid ? cq : INT32_MIN));
+        int mn = INT32_MAX, mx = INT32_MIN;
+#pragma unroll
+        for (int r = 0; r < (32 * W + 63) / 64; ++r) {
+            const int qq = qw0 + r * 64 + lane;
+            if (r * 64 + lane < 32 * W && qq < L) {
+                const int c = p.chain_id[(int64_t)b * L + qq];
+                mn = min(mn, c);
+                mx = max(mx, c);
+            }
+        }
+        wq_min = __builtin_amdgcn_readfirstlane(wave_min_i(mn));
+        wq_max = __builtin_amdgcn_readfirstlane(wave_max_i(mx));
     }
     const uint8_t* mrow = nullptr;
     if constexpr (DENSE) {
         mrow = p.chain_mask + (int64_t)b * p.mask_stride_b + (int64_t)(qvalid ? q : 0) * p.mask_stride_q;
     }
 
-    // ---- online softmax state ----
-    // Logits are handled in base-2 units, s2 = c * s. With BIAS (fused RoPE) c
-    // is folded into Q in fp32 before its single rounding, and the MFMA itself
-    // returns s2 - m_ref through one extra feature (K side 1, Q side -m_ref,
-    // m_ref kept bf16-exact): no per-logit FMA. Without BIAS (caller-rotated
-    // q/k used as given) s2 - m_ref is one FMA per logit.
-    // The bias feature costs one more MFMA on each subtile's dependency chain
-    // (QK -> bias -> max -> exp); measured on MI355X at the 150M shape it is
-    // slower (182 us vs 153 us) than one FMA per logit, so it stays off.
-    constexpr bool BIAS = false;
-    const float c = args.c;  // 1 with BIAS
-    float m_ref = 0.f;       // reference max (base 2)
-    bool started = false;    // wave-uniform: m_ref has been set
+    // ---- softmax state ----
+    // Probabilities are exp2(s2 - m_ref) with s2 = c * s the base-2 logit.
+    // m_ref starts at 0 and stays there unless a stage's row sum leaves
+    // (0, 2^64]: then the fix-up path sets it from that stage's max and the
+    // wavefront switches to the shifted form (one FMA per logit).
+    const float c = args.c;  // 1 when FOLDED
+    float m_ref = 0.f;
+    bool shifted = false;    // wavefront-uniform: some m_ref != 0
     float l_run = 0.f;
     f32x16 o[S::NDB];
 #pragma unroll
@@ -332,45 +335,22 @@ void fwd_kernel(const FwdArgs args) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
 
-    // K operand row: subtile row ql with bits 2,3 swapped.
-    const int krow = (ql & ~12) | ((ql & 4) << 1) | ((ql & 8) >> 1);
-    v8 zero8, one8, unit8;
+    const int krow = swapped_row(ql);
+    v8 zero8;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        zero8[t] = (T)0.f;
-        one8[t] = (T)1.0f;
-        unit8[t] = (T)(t == 0 ? 1.0f : 0.0f);
-    }
-    // Bias feature: an extra K-chunk (K side: 1 at dim 0 of lane half 0) for
-    // D != 24; for D = 24 it is dim 24, inside the zero padding [24, 32).
-    const v8 kbias = hh == 0 ? unit8 : zero8;
-    v8 qbias = zero8;
-    auto set_bias = [&]() {
-        const T nb = (T)(-m_ref);
-        if constexpr (D == 24) {
-            if (hh) {
-                qf[0][1][0] = nb;
-                qf[1][1][0] = nb;
-            }
-        } else {
-            if (hh == 0) qbias[0] = nb;
-        }
-    };
+    for (int t = 0; t < 8; ++t) zero8[t] = (T)0.f;
 
-    // Per-lane LDS byte offsets of the MFMA operands inside a tile. The chunk
-    // swizzle repeats every 16 rows, so moving to another subtile or key chunk
-    // only adds a constant.
-    // K operand (A of S^T = K Q^T): row krow, dims kk*16 + 8*hh + [0, 8).
+    // Per-lane LDS byte offsets of the MFMA operands inside a tile (the chunk
+    // swizzle repeats every 16 rows, so other subtiles only add a constant).
     int koff[S::NKK];
 #pragma unroll
     for (int kk = 0; kk < S::NKK; ++kk) {
         const int cch = 2 * kk + hh;
         koff[kk] = cch < S::NCH ? krow * S::RB + S::swz(krow, cch) * 16 : 0;
     }
-    // V operand (A of O^T += V^T P^T) for d block db via ds_read_b64_tr_b16:
-    // lane (group tg, index ti) addresses row 8*(tg>>1) + 4*rr + ti/4 and the
-    // 8-byte chunk 8*db + 4*(tg&1) + ti%4 (clamped into the row when D = 24/16;
-    // those lanes' results are replaced by the ones rows).
+    // V^T operand via ds_read_b64_tr_b16: lane (group tg, index ti) addresses
+    // row 8*(tg>>1) + 4*rr + ti/4 and the 8-byte chunk 8*db + 4*(tg&1) + ti%4
+    // (clamped into the row for D < 32; those lanes' values are unused).
     const int tg = lane >> 4, ti = lane & 15;
     int voffv[S::NDB][2];
 #pragma unroll
@@ -384,257 +364,364 @@ void fwd_kernel(const FwdArgs args) {
         }
     }
 
-    auto kop = [&](const char* stage, int ten, int st, int kk) -> v8 {
-        if (2 * kk + hh >= S::NCH) return BIAS ? unit8 : zero8;  // D = 24: dims [24, 32)
-        return *reinterpret_cast<const v8*>(stage + ten * S::TILE + st * 32 * S::RB + koff[kk]);
+    // Base-2 probability of raw logit x.
+    auto prob = [&](float x, bool sh) -> float {
+        if (sh) return fast_exp2(fmaf(x, c, -m_ref));
+        return fast_exp2(FOLDED ? x : x * c);
     };
-    auto vop = [&](const char* stage, int ten, int st, int cc, int db) -> v8 {
-        const int d = db * 32 + (lane & 31);
-        s4 half[2];
+    // Probabilities of NS subtiles (slot 8*cc + t -> pb[st][cc][t]) and their
+    // row sum over this lane's keys.
+    auto probs = [&](auto ns_c, const f32x16* sv, v8 (*pb)[2], bool sh) -> float {
+        constexpr int NS = decltype(ns_c)::value;
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        // Pairs are rounded once (v_cvt_pk) and feed both the PV operand and
+        // the row sum; two sum chains halve the dependency depth.
+        float ls0 = 0.f, ls1 = 0.f;
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr) {
-            const char* ptr = stage + ten * S::TILE + (st * 32 + 16 * cc) * S::RB + voffv[db][rr];
-            half[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(ptr));
-        }
-        // Whole-vector bitcast: element-wise i16 -> bf16 inserts are mis-lowered.
-        const v8 r8 = __builtin_bit_cast(v8, __builtin_shufflevector(half[0], half[1], 0, 1, 2, 3, 4, 5, 6, 7));
-        if constexpr (D % 32 == 0) return r8;
-        return d < D ? r8 : one8;
+        for (int st = 0; st < NS; ++st)
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                v2 pr[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const f32x2 f = {prob(sv[st][8 * cc + 2 * u], sh), prob(sv[st][8 * cc + 2 * u + 1], sh)};
+                    pr[u] = __builtin_convertvector(f, v2);
+                }
+                pb[st][cc] = __builtin_shufflevector(__builtin_shufflevector(pr[0], pr[1], 0, 1, 2, 3),
+                                                     __builtin_shufflevector(pr[2], pr[3], 0, 1, 2, 3), 0, 1, 2,
+                                                     3, 4, 5, 6, 7);
+                ls0 = E::sum2(pr[0], ls0);
+                ls1 = E::sum2(pr[1], ls1);
+                ls0 = E::sum2(pr[2], ls0);
+                ls1 = E::sum2(pr[3], ls1);
+            }
+        return ls0 + ls1;
     };
-    // S^T of one subtile for pathway pw from preloaded K operands.
-    auto qk = [&](const v8* ka, int pw) -> f32x16 {
-        f32x16 sv;
+    // Rare path: a lane's stage sum overflowed, or its row has accumulated
+    // nothing yet. The stage's logits are recomputed from LDS (`logits`
+    // fills sv) and its probabilities redone relative to a reference max
+    // taken from them (raised only, once something has been accumulated).
+    auto fixup = [&](auto ns_c, auto logits, v8 (*pb)[2]) -> float {
+        constexpr int NS = decltype(ns_c)::value;
+        f32x16 sv[NS];
+        logits(sv);
+        float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sv[i] = 0.f;
+        for (int st = 0; st < NS; ++st)
 #pragma unroll
-        for (int kk = 0; kk < S::NKK; ++kk) sv = E::mma(ka[kk], qf[pw][kk], sv);
-        if constexpr (BIAS && D != 24) sv = E::mma(kbias, qbias, sv);
-        return sv;
-    };
-
-    // Reference-max update. `rel` is this lane half's max of s2 - m_ref over
-    // the new logits. Rescales (rarely) when a row max exceeds the reference
-    // by 2^8; the first stage only sets the reference. Returns true if m_ref
-    // moved, with `shift` = new - old (BIAS logits must subtract it).
-    auto update = [&](float rel, float& shift) -> bool {
-        shift = 0.f;
-        const bool need = !started || rel > 8.0f;
-        if (__builtin_amdgcn_ballot_w64(need) == 0) return false;
-        const float ra = fmaxf(rel, __shfl_xor(rel, 32));
-        const bool upd = !started || ra > 8.0f;
-        float m_new = upd ? m_ref + ra : m_ref;
-        if constexpr (BIAS) m_new = (float)(T)m_new;
-        shift = m_new - m_ref;
-        const float alpha = started ? fast_exp2(-shift) : 0.f;
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sv[st][i]);
+        const float mq = fmaxf(mx, __shfl_xor(mx, 32));  // query max of the stage, raw units
+        const float lq = l_run + __shfl_xor(l_run, 32);
+        const float ms = mq * c;
+        float m_new;
+        if (lq > 0.f) m_new = fmaxf(m_ref, ms);
+        else m_new = ms > -INFINITY ? ms : m_ref;
+        const float alpha = lq > 0.f ? fast_exp2(m_ref - m_new) : 1.0f;
         l_run *= alpha;
 #pragma unroll
         for (int db = 0; db < S::NDB; ++db)
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
         m_ref = m_new;
-        started = true;
-        if constexpr (BIAS) set_bias();
-        return true;
+        shifted = __builtin_amdgcn_ballot_w64(m_ref != 0.f) != 0;
+        return probs(ns_c, sv, pb, true);
+    };
+    // Stage check: true if any lane needs the fix-up.
+    auto needs_fix = [&](float ls) {
+        const bool bad = !(ls <= kSumHi) || (l_run + ls == 0.f);
+        return __builtin_amdgcn_ballot_w64(bad) != 0;
     };
 
-    // One pathway over NS consecutive subtiles starting at subtile st0.
-    auto pure = [&](auto pw_c, auto ns_c, const char* stage, int st0) {
-        constexpr int pw = decltype(pw_c)::value;
-        constexpr int NS = decltype(ns_c)::value;
-        // All LDS operands of the step are read up front: the V reads then
-        // overlap the softmax.
-        v8 ka[NS][S::NKK], va[NS][2][S::NDB];
+    // Operand readers with the tile base given.
+    auto kop_t = [&](const char* tile, int st, int kk) -> v8 {
+        if (2 * kk + hh >= S::NCH) return zero8;  // D = 24: dims [24, 32)
+        return *reinterpret_cast<const v8*>(tile + st * 32 * S::RB + koff[kk]);
+    };
+    auto vop_t = [&](const char* tile, int st, int cc, int db) -> v8 {
+        s4 half[2];
 #pragma unroll
-        for (int st = 0; st < NS; ++st)
+        for (int rr = 0; rr < 2; ++rr) {
+            const char* ptr = tile + (st * 32 + 16 * cc) * S::RB + voffv[db][rr];
+            half[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(ptr));
+        }
+        // Whole-vector bitcast: element-wise i16 -> bf16 inserts are mis-lowered.
+        return __builtin_bit_cast(v8, __builtin_shufflevector(half[0], half[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    // S^T of one subtile from K operands ka and Q operands qa.
+    auto qkq = [&](const v8* ka, const v8* qa) -> f32x16 {
+        f32x16 sv;
 #pragma unroll
-            for (int kk = 0; kk < S::NKK; ++kk) ka[st][kk] = kop(stage, pw, st0 + st, kk);
+        for (int i = 0; i < 16; ++i) sv[i] = 0.f;
 #pragma unroll
-        for (int st = 0; st < NS; ++st)
+        for (int kk = 0; kk < S::NKK; ++kk) sv = E::mma(ka[kk], qa[kk], sv);
+        return sv;
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+
+    // Q operand of the fast path's pathway (changes rarely: at chain edges).
+    int cur_pw = 0;
+    v8 qcur[S::NKK];
+#pragma unroll
+    for (int kk = 0; kk < S::NKK; ++kk) qcur[kk] = qf[0][kk];
+
+    // Fast path: both subtiles of the stage on pathway pw, unshifted softmax.
+    // Returns false (nothing accumulated) if the stage needs the fix-up.
+    auto fast_stage = [&](const char* stage, int pw) -> bool {
+        const char* kt = stage + pw * S::TILE;
+        const char* vt = stage + (2 + pw) * S::TILE;
+        // All LDS operands are read up front: the V reads overlap the softmax.
+        v8 ka[2][S::NKK], va[2][2][S::NDB];
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int kk = 0; kk < S::NKK; ++kk) ka[st][kk] = kop_t(kt, st, kk);
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-                for (int db = 0; db < S::NDB; ++db) va[st][cc][db] = vop(stage, 2 + pw, st0 + st, cc, db);
-        f32x16 sv[NS];
+                for (int db = 0; db < S::NDB; ++db) va[st][cc][db] = vop_t(vt, st, cc, db);
+        // keep every LDS read of the stage ahead of the softmax
+        __builtin_amdgcn_sched_barrier(0);
+        v8 pb[2][2];
+        float ls;
+        {
+            f32x16 sv[2];
 #pragma unroll
-        for (int st = 0; st < NS; ++st) sv[st] = qk(ka[st], pw);
-        float mx = sv[0][0];
-#pragma unroll
-        for (int st = 0; st < NS; ++st)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sv[st][i]);
-        float shift;
-        const bool moved = update(BIAS ? mx : fmaf(mx, c, -m_ref), shift);
-        if constexpr (BIAS) {
-            if (moved) {
-#pragma unroll
-                for (int st = 0; st < NS; ++st)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) sv[st][i] -= shift;
-            }
+            for (int st = 0; st < 2; ++st) sv[st] = qkq(ka[st], qcur);
+            ls = probs(I2{}, sv, pb, false);
         }
-        const float mc = m_ref;
+        if (needs_fix(ls)) return false;
+        l_run += ls;
 #pragma unroll
-        for (int st = 0; st < NS; ++st) {
+        for (int st = 0; st < 2; ++st)
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                float pr[8];
+            for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-                for (int t = 0; t < 8; ++t)
-                    pr[t] = fast_exp2(BIAS ? sv[st][8 * cc + t] : fmaf(sv[st][8 * cc + t], c, -mc));
-                const v8 pb = pack8<T>(pr);
-                if constexpr (!S::SUM_MFMA) {
-#pragma unroll
-                    for (int t = 0; t < 8; t += 2) l_run = E::sum2(v2{pb[t], pb[t + 1]}, l_run);
-                }
-#pragma unroll
-                for (int db = 0; db < S::NDB; ++db) o[db] = E::mma(va[st][cc][db], pb, o[db]);
-            }
-        }
+                for (int db = 0; db < S::NDB; ++db) o[db] = E::mma(va[st][cc][db], pb[st][cc], o[db]);
+        return true;
     };
 
     // Both pathways on one subtile, selected per element; handles padded keys.
     auto general = [&](const char* stage, const int* cid, int st, int k0) {
-        v8 ks[S::NKK], km[S::NKK];
-#pragma unroll
-        for (int kk = 0; kk < S::NKK; ++kk) {
-            ks[kk] = kop(stage, 0, st, kk);
-            km[kk] = kop(stage, 1, st, kk);
-        }
-        const f32x16 ss = qk(ks, 0), sm = qk(km, 1);
-        f32x16 sv;
         bool same[16];
-        // keys of slot i: st*32 + 16*(i/8) + 8*hh + i%8
+        // Selected raw logits (-inf for padded keys) into sv[0]; keys of
+        // slot i: st*32 + 16*(i/8) + 8*hh + i%8.
+        auto logits = [&](f32x16* sv) {
+            v8 ks[S::NKK], km[S::NKK];
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            const int kl = st * 32 + 16 * cc + 8 * hh;
-            const i32x4 c0 = *reinterpret_cast<const i32x4*>(&cid[kl]);
-            const i32x4 c1 = *reinterpret_cast<const i32x4*>(&cid[kl + 4]);
-            uint32_t mbits = 0;
-            if constexpr (DENSE) {
-                const int kg = k0 + kl;
-                for (int t = 0; t < 8; ++t)
-                    if (kg + t < L)
-                        mbits |= (uint32_t)(mrow[(int64_t)(kg + t) * p.mask_stride_k] != 0) << t;
+            for (int kk = 0; kk < S::NKK; ++kk) {
+                ks[kk] = kop_t(stage, st, kk);
+                km[kk] = kop_t(stage + S::TILE, st, kk);
             }
+            const f32x16 ss = qkq(ks, qf[0]), sm = qkq(km, qf[1]);
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const int ck = t < 4 ? c0[t & 3] : c1[t & 3];
-                const int i = 8 * cc + t;
-                const bool sm_ = DENSE ? !((mbits >> t) & 1u) : (ck == cq);
-                same[i] = sm_;
-                const float v = sm_ ? ss[i] : sm[i];
-                sv[i] = ck == kPadChain ? -INFINITY : v;
+            for (int cc = 0; cc < 2; ++cc) {
+                const int kl = st * 32 + 16 * cc + 8 * hh;
+                const i32x4 c0 = *reinterpret_cast<const i32x4*>(&cid[kl]);
+                const i32x4 c1 = *reinterpret_cast<const i32x4*>(&cid[kl + 4]);
+                uint32_t mbits = 0;
+                if constexpr (DENSE) {
+                    const int kg = k0 + kl;
+                    for (int t = 0; t < 8; ++t)
+                        if (kg + t < L)
+                            mbits |= (uint32_t)(mrow[(int64_t)(kg + t) * p.mask_stride_k] != 0) << t;
+                }
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int ck = t < 4 ? c0[t & 3] : c1[t & 3];
+                    const int i = 8 * cc + t;
+                    const bool sm_ = DENSE ? !((mbits >> t) & 1u) : (ck == cq);
+                    same[i] = sm_;
+                    const float v = sm_ ? ss[i] : sm[i];
+                    sv[0][i] = ck == kPadChain ? -INFINITY : v;
+                }
             }
+        };
+        v8 pb[1][2];
+        float ls;
+        {
+            f32x16 sv[1];
+            logits(sv);
+            ls = shifted ? probs(I1{}, sv, pb, true) : probs(I1{}, sv, pb, false);
         }
-        float mx = sv[0];
-#pragma unroll
-        for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
-        float shift;
-        const bool moved = update(BIAS ? mx : fmaf(mx, c, -m_ref), shift);
-        if constexpr (BIAS) {
-            if (moved) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) sv[i] -= shift;
-            }
-        }
-        const float mc = m_ref;
+        if (needs_fix(ls)) ls = fixup(I1{}, logits, pb);
+        l_run += ls;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
             v8 ps, pm;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 const int i = 8 * cc + t;
-                const T pv = (T)fast_exp2(BIAS ? sv[i] : fmaf(sv[i], c, -mc));
-                ps[t] = same[i] ? pv : (T)0.f;
-                pm[t] = same[i] ? (T)0.f : pv;
-            }
-            if constexpr (!S::SUM_MFMA) {
-#pragma unroll
-                for (int t = 0; t < 8; t += 2) {
-                    l_run = E::sum2(v2{ps[t], ps[t + 1]}, l_run);
-                    l_run = E::sum2(v2{pm[t], pm[t + 1]}, l_run);
-                }
+                ps[t] = same[i] ? pb[0][cc][t] : (T)0.f;
+                pm[t] = same[i] ? (T)0.f : pb[0][cc][t];
             }
 #pragma unroll
             for (int db = 0; db < S::NDB; ++db) {
-                o[db] = E::mma(vop(stage, 2, st, cc, db), ps, o[db]);
-                o[db] = E::mma(vop(stage, 3, st, cc, db), pm, o[db]);
+                o[db] = E::mma(vop_t(stage + 2 * S::TILE, st, cc, db), ps, o[db]);
+                o[db] = E::mma(vop_t(stage + 3 * S::TILE, st, cc, db), pm, o[db]);
             }
         }
     };
 
-    auto subtile_mode = [&](int kmin, int kmax, int npad) {
-        // 0: pure self, 1: pure multimer, 2: general, 3: skip (all padded)
-        if (npad == 32) return 3;
-        if (!DENSE && npad == 0) {
-            if (kmin == kmax && cq_min == cq_max && kmin == cq_min) return 0;
-            if (kmax < cq_min || kmin > cq_max) return 1;
+    // One subtile on the slow path. code: 0 pure self, 1 pure multimer,
+    // 2 straddle (keys on one chain, queries on several: pathway per lane),
+    // 3 general, 4 skip.
+    auto slow_subtile = [&](const char* stage, const int* cid, int st, int code, int k0) {
+        if (code >= 4) return;
+        if (code == 3) {
+            general(stage, cid, st, k0);
+            return;
         }
-        return 2;
+        v8 pb[1][2];
+        float ls;
+        if (code <= 1) {
+            const int pw = code;
+            const char* kt = stage + pw * S::TILE;
+            v8 qa[S::NKK];
+#pragma unroll
+            for (int kk = 0; kk < S::NKK; ++kk) qa[kk] = pw ? qf[1][kk] : qf[0][kk];
+            auto logits = [&](f32x16* sv) {
+                v8 kr[S::NKK];
+#pragma unroll
+                for (int kk = 0; kk < S::NKK; ++kk) kr[kk] = kop_t(kt, st, kk);
+                sv[0] = qkq(kr, qa);
+            };
+            {
+                f32x16 sv[1];
+                logits(sv);
+                ls = shifted ? probs(I1{}, sv, pb, true) : probs(I1{}, sv, pb, false);
+            }
+            if (needs_fix(ls)) ls = fixup(I1{}, logits, pb);
+            l_run += ls;
+            const char* vt = stage + (2 + pw) * S::TILE;
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+                for (int db = 0; db < S::NDB; ++db) o[db] = E::mma(vop_t(vt, st, cc, db), pb[0][cc], o[db]);
+            return;
+        }
+        // straddle: lane is on the self pathway iff its chain is the keys' chain
+        const bool self_lane = cq == cid[st * 32];
+        auto logits = [&](f32x16* sv) {
+            v8 ks[S::NKK], km[S::NKK];
+#pragma unroll
+            for (int kk = 0; kk < S::NKK; ++kk) {
+                ks[kk] = kop_t(stage, st, kk);
+                km[kk] = kop_t(stage + S::TILE, st, kk);
+            }
+            const f32x16 ss = qkq(ks, qf[0]), sm = qkq(km, qf[1]);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sv[0][i] = self_lane ? ss[i] : sm[i];
+        };
+        {
+            f32x16 sv[1];
+            logits(sv);
+            ls = shifted ? probs(I1{}, sv, pb, true) : probs(I1{}, sv, pb, false);
+        }
+        if (needs_fix(ls)) ls = fixup(I1{}, logits, pb);
+        l_run += ls;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const v8 ps = self_lane ? pb[0][cc] : zero8;
+            const v8 pm = self_lane ? zero8 : pb[0][cc];
+#pragma unroll
+            for (int db = 0; db < S::NDB; ++db) {
+                o[db] = E::mma(vop_t(stage + 2 * S::TILE, st, cc, db), ps, o[db]);
+                o[db] = E::mma(vop_t(stage + 3 * S::TILE, st, cc, db), pm, o[db]);
+            }
+        }
     };
 
-    // Pathway codes of 64 consecutive 32-key subtiles starting at kb0, as two
-    // bit masks (bit k of mlo / mhi = low / high bit of subtile kb0 + k).
-    uint64_t mlo = 0, mhi = 0;
+    auto subtile_mode = [&](int kmin, int kmax, int npad) -> int {
+        if (npad == 32) return 4;
+        if (DENSE) return 3;
+        if (npad == 0) {
+            if (kmax < cq_min || kmin > cq_max) return 1;
+            if (kmin == kmax) return cq_min == cq_max ? 0 : 2;
+        }
+        return 3;
+    };
+
+    // For 64 consecutive 32-key subtiles from kb0: this wavefront's subtile
+    // codes as three bit masks (mb0..mb2 = code bits), and which pathways the
+    // workgroup needs (nS / nM) so stages copy only those tiles.
+    uint64_t mb0 = 0, mb1 = 0, mb2 = 0, nS = 0, nM = 0;
     auto load_modes = [&](int kb0) {
         const int kb = kb0 + lane;
-        int code = 3;
+        int code = 4;
+        bool ns = false, nm = false;
         if (kb < Lp / 32) {
             const int4 sm = ksum_b[kb];
             code = subtile_mode(sm.x, sm.y, sm.z);
+            if (sm.z < 32) {
+                if (DENSE || sm.z > 0) {
+                    ns = nm = true;
+                } else {
+                    ns = !(sm.y < wq_min || sm.x > wq_max);
+                    nm = !(sm.x == sm.y && wq_min == wq_max && sm.x == wq_min);
+                }
+            }
         }
-        mlo = __builtin_amdgcn_ballot_w64(code & 1);
-        mhi = __builtin_amdgcn_ballot_w64((code >> 1) & 1);
+        mb0 = __builtin_amdgcn_ballot_w64(code & 1);
+        mb1 = __builtin_amdgcn_ballot_w64((code >> 1) & 1);
+        mb2 = __builtin_amdgcn_ballot_w64((code >> 2) & 1);
+        nS = __builtin_amdgcn_ballot_w64(ns);
+        nM = __builtin_amdgcn_ballot_w64(nm);
+    };
+    auto code_at = [&](int sub) -> int {
+        return (int)((mb0 >> sub) & 1) | (int)(((mb1 >> sub) & 1) << 1) | (int)(((mb2 >> sub) & 1) << 2);
     };
 
     // ---- main loop over stages ----
     const int nst = (L + kBN - 1) / kBN;
+    int kbase = 0;  // first subtile covered by the masks
     load_modes(0);  // before any copy is in flight (its wait drains vmcnt)
-#pragma unroll
-    for (int t = 0; t < NBUF - 1; ++t)
-        if (t < nst) issue(t, t);
+    // Tiles a stage copies (bit t = tile t): K_self and V_self (bits 0, 2)
+    // if any subtile needs the self pathway, K_multi and V_multi (1, 3) for
+    // the multimer pathway.
+    auto tiles_of = [&](int nx) -> int {
+        const int t = (((nS >> nx) & 3) != 0 ? 5 : 0) | (((nM >> nx) & 3) != 0 ? 10 : 0);
+        return __builtin_amdgcn_readfirstlane(t);
+    };
+    issue(0, 0, tiles_of(0));
     for (int s = 0; s < nst; ++s) {
-        const int bf = s % NBUF;
-        if constexpr (NBUF == 3) {
-            if (s + 1 < nst) wait_vm<IPW>();
-            else wait_vm<0>();
-        } else {
-            wait_vm<0>();
-        }
+        const int bf = s & 1;
+        wait_vm<0>();
         stage_barrier();
-        if (s + NBUF - 1 < nst) issue(s + NBUF - 1, (s + NBUF - 1) % NBUF);
+        const int sub = 2 * s - kbase;
+        const int c0 = code_at(sub), c1 = code_at(sub + 1);
+        if (s + 1 < nst) {
+            if (2 * (s + 1) - kbase >= 64) {  // no copy in flight here
+                kbase = 2 * (s + 1);
+                load_modes(kbase);
+            }
+            const int nx = 2 * (s + 1) - kbase;
+            issue(s + 1, bf ^ 1, tiles_of(nx));
+        }
 
-        if (s > 0 && (s & 31) == 0) load_modes(2 * s);
-        const int sub = (2 * s) & 63;
-        const int m0 = (int)((mlo >> sub) & 1) | (int)(((mhi >> sub) & 1) << 1);
-        const int m1 = (int)((mlo >> (sub + 1)) & 1) | (int)(((mhi >> (sub + 1)) & 1) << 1);
         const char* stage = smem + bf * S::STAGE;
-        const int* cid = &scid[wave][bf][0];
-        const int k0 = s * kBN;
-        using I0 = std::integral_constant<int, 0>;
-        using I1 = std::integral_constant<int, 1>;
-        using I2 = std::integral_constant<int, 2>;
-        if (m0 == 0 && m1 == 0) {
-            pure(I0{}, I2{}, stage, 0);
-        } else if (m0 == 1 && m1 == 1) {
-            pure(I1{}, I2{}, stage, 0);
-        } else {
-            if (m0 == 0) pure(I0{}, I1{}, stage, 0);
-            else if (m0 == 1) pure(I1{}, I1{}, stage, 0);
-            else if (m0 == 2) general(stage, cid, 0, k0);
-            if (m1 == 0) pure(I0{}, I1{}, stage, 1);
-            else if (m1 == 1) pure(I1{}, I1{}, stage, 1);
-            else if (m1 == 2) general(stage, cid, 1, k0);
+        bool done = false;
+        if (c0 == c1 && c0 <= 1 && !shifted) {
+            if (c0 != cur_pw) {  // rare: kept a branch (not selects on every stage)
+                asm volatile("" ::: "memory");
+                cur_pw = c0;
+#pragma unroll
+                for (int kk = 0; kk < S::NKK; ++kk) qcur[kk] = c0 ? qf[1][kk] : qf[0][kk];
+            }
+            done = fast_stage(stage, c0);
+        }
+        if (!done) {
+            const int* cid = &scid[wave][bf][0];
+            const int k0 = s * kBN;
+#pragma unroll 1
+            for (int st = 0; st < 2; ++st) slow_subtile(stage, cid, st, st ? c1 : c0, k0);
         }
     }
 
     // ---- epilogue: normalise, store O and LSE ----
-    float l_tot;
-    if constexpr (S::SUM_MFMA) {
-        l_tot = o[0][S::ISUM];
-    } else {
-        l_tot = l_run + __shfl_xor(l_run, 32);
-    }
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     if (qvalid) {
         T* orow = (T*)p.out.ptr + b * p.out.stride_b + h * p.out.stride_h + (int64_t)q * p.out.stride_t;
@@ -659,8 +746,7 @@ void fwd_kernel(const FwdArgs args) {
 
 template <typename T, int D, bool ROPE, bool DENSE>
 static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
-    constexpr int W = 4;
-    constexpr int NBUF = D <= 32 ? MPATTN_FWD_NBUF32 : 2;
+    constexpr int W = FwdShape<D>::W;
     const mpattn_fwd_params& p = a.p;
     const int Lp = round_up(p.L, kBN);
     a.Lp = Lp;
@@ -681,8 +767,7 @@ static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     const int nqb = (p.L + 32 * W - 1) / (32 * W);
     const int64_t grid = (int64_t)p.B * p.H * nqb;
-    hipLaunchKernelGGL((fwd_kernel<T, D, W, NBUF, ROPE, DENSE>), dim3((unsigned)grid), dim3(W * 64), 0,
-                       stream, a);
+    hipLaunchKernelGGL((fwd_kernel<T, D, W, ROPE, DENSE>), dim3((unsigned)grid), dim3(W * 64), 0, stream, a);
     return hipGetLastError();
 }
 
