@@ -12,32 +12,33 @@
 //    with fused RoPE, K_self rotated once into the workspace.
 //
 // 2. fwd_kernel:
-//  * A workgroup of W wavefronts owns 32*W consecutive queries of one (b, h);
-//    each wavefront owns 32 of them. Q is loaded once, RoPE and the logit
-//    scale applied in fp32.
-//  * Keys stream through a ring of NBUF LDS stages of 64 keys. Each stage holds
-//    K_self, K_multi, V_self, V_multi tiles copied by global_load_lds (16 bytes
-//    per lane, straight into LDS, no register round trip), issued NBUF-1
-//    stages ahead of use, one barrier per stage. Rows are stored densely with
+//  * A workgroup of W wavefronts (8 for D <= 32) owns 32*W consecutive queries
+//    of one (b, h); each wavefront owns 32 of them. Q is loaded once, RoPE and
+//    the logit scale applied in fp32.
+//  * Keys stream through a ring of NBUF LDS stages of 64 keys. A stage has
+//    room for K_self, K_multi, V_self, V_multi tiles, copied by
+//    global_load_lds (16 bytes per lane, straight into LDS); only the tiles of
+//    the pathways some wavefront of the workgroup needs are copied. Copies run
+//    NBUF-1 stages ahead; one barrier per stage. Rows are stored densely with
 //    their 16-byte chunks XOR-swizzled by row to spread LDS banks.
 //  * Per 32-key subtile a wavefront computes S^T = K Q^T with
 //    v_mfma_f32_32x32x16 (rows = keys, columns = queries): lane l holds 16
-//    logits of query l%32, so the softmax row statistics are in-lane. K rows
-//    are read with bits 2 and 3 of the row index swapped, which makes
-//    accumulator slot i of lane half hh the key 16*(i/8) + 8*hh + i%8: the
-//    probabilities are then already the B operand of O^T += V^T P^T. The V^T
-//    operand comes from the row-major V tile via ds_read_b64_tr_b16.
-//  * Stages are classified from the per-32-key chain summaries and the
-//    wavefront's query chain range: pure same-chain stages run only the self
-//    pathway, pure cross-chain stages only the multimer pathway (one softmax
-//    update over 64 keys); mixed or padded subtiles compute both logits and
-//    select per element.
-//  * Online softmax in base 2 with a lazily updated reference max: nothing is
-//    rescaled unless a row max grows by more than 2^8, and only then do the
-//    two lane halves of a query exchange their maxima.
+//    logits of query l%32, so the softmax statistics are in-lane. K rows are
+//    read with bits 2 and 3 of the row index swapped, which makes accumulator
+//    slot i of lane half hh the key 16*(i/8) + 8*hh + i%8: the probabilities
+//    are then already the B operand of O^T += V^T P^T. The V^T operand comes
+//    from the row-major V tile via ds_read_b64_tr_b16.
+//  * Subtiles are classified from per-32-key and per-32-query chain summaries:
+//    pure self / pure multimer (one pathway), straddle (keys on one chain,
+//    queries on several: pathway chosen per lane), general (mixed or padded
+//    keys: both logits, selected per element), skip (all keys padded). Stages
+//    whose two subtiles share one pure pathway take the fast path.
+//  * Softmax in base 2 without a running max: p = exp2(s2) relative to a
+//    reference m_ref = 0. A stage whose row sum leaves (0, 2^64] takes a rare
+//    fix-up path that recomputes it against the stage's max and moves m_ref
+//    (the wavefront then subtracts m_ref with one FMA per logit).
 //  * Row sums come from v_dot2_f32_bf16 on the rounded probabilities (the
-//    values the PV MFMA consumes). For D < 32 the unused rows of the V^T
-//    operand are ones, so the MFMA produces the sum.
+//    values the PV MFMA consumes).
 #include <type_traits>
 
 #include "mpattn_common.h"
@@ -50,10 +51,11 @@ inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
 // Workspace layout (offsets 256-byte aligned):
 //   keff int32 [B][Lp]          effective chain id per key
-//   ksum int32 [B][Lp/32][4]    min chain, max chain, #padded, 0
+//   ksum int32 [B][Lp/32][4]    keys: min chain, max chain (valid keys), #padded, 0
+//   qsum int32 [B][Lp/32][4]    queries: min chain, max chain (queries < L), 0, 0
 //   krot T     [B][H][Lp][D]    RoPE-rotated K_self (fused RoPE only)
 struct FwdWs {
-    int64_t keff, ksum, krot, total;
+    int64_t keff, ksum, qsum, krot, total;
 };
 
 inline FwdWs fwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
@@ -62,7 +64,8 @@ inline FwdWs fwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
     FwdWs w;
     w.keff = 0;
     w.ksum = al(w.keff + (int64_t)B * Lp * 4);
-    w.krot = al(w.ksum + (int64_t)B * (Lp / 32) * 16);
+    w.qsum = al(w.ksum + (int64_t)B * (Lp / 32) * 16);
+    w.krot = al(w.qsum + (int64_t)B * (Lp / 32) * 16);
     w.total = al(w.krot + (rope ? (int64_t)B * H * Lp * D * esize : 0));
     return w;
 }
@@ -76,6 +79,7 @@ struct FwdArgs {
     mpattn_fwd_params p;
     const int* keff;
     const int* ksum;
+    const int* qsum;
     const void* krot;
     int Lp;
     float qmul;    // factor applied to q while loading (scale*log2e when fused, else 1)
@@ -87,7 +91,7 @@ struct FwdArgs {
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool ROPE, bool DENSE>
 __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p, int* keff,
-                                                       int* ksum, T* krot, int Lp, int nchain) {
+                                                       int* ksum, int* qsum, T* krot, int Lp, int nchain) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int L = p.L;
     if ((int)blockIdx.x < nchain) {
@@ -96,21 +100,29 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p
         if (gid >= p.B * ngrp) return;
         const int b = gid / ngrp, k0 = (gid % ngrp) * 64;
         const int kg = k0 + lane;
+        const int chain = kg < L && !DENSE ? p.chain_id[(int64_t)b * L + kg] : 0;
         int cid = kPadChain;
-        if (kg < L && !(p.key_pad && p.key_pad[(int64_t)b * L + kg]))
-            cid = DENSE ? 0 : p.chain_id[(int64_t)b * L + kg];
+        if (kg < L && !(p.key_pad && p.key_pad[(int64_t)b * L + kg])) cid = chain;
         keff[(int64_t)b * Lp + kg] = cid;
         const bool valid = cid != kPadChain;
         const int mn = half_min_i(valid ? cid : INT32_MAX);
         const int mx = half_max_i(valid ? cid : INT32_MIN);
         const uint64_t padm = __ballot(!valid);
+        const int qmn = half_min_i(kg < L ? chain : INT32_MAX);
+        const int qmx = half_max_i(kg < L ? chain : INT32_MIN);
         if ((lane & 31) == 0) {
             const int hh = lane >> 5;
-            int* o = ksum + ((int64_t)b * (Lp / 32) + (k0 >> 5) + hh) * 4;
+            const int64_t blk = (int64_t)b * (Lp / 32) + (k0 >> 5) + hh;
+            int* o = ksum + blk * 4;
             o[0] = mn;
             o[1] = mx;
             o[2] = __popcll(hh ? (padm >> 32) : (padm & 0xffffffffull));
             o[3] = 0;
+            int* oq = qsum + blk * 4;
+            oq[0] = qmn;
+            oq[1] = qmx;
+            oq[2] = 0;
+            oq[3] = 0;
         }
         return;
     }
@@ -177,13 +189,25 @@ template <int D> struct FwdShape : TileShape<D> {
 #ifndef MPATTN_FWD_WAVES
 #define MPATTN_FWD_WAVES 4  // register budget: wavefronts per SIMD
 #endif
+#ifndef MPATTN_FWD_NBUF
+#define MPATTN_FWD_NBUF 2  // LDS stages in the copy ring (copies run NBUF-1 stages ahead)
+#endif
+#ifndef MPATTN_FWD_SPLIT
+// Key halves per 32-query block (D <= 32). 2 fills the machine in whole rounds
+// at the 150M shape but doubles the per-task prologue and the L2->LDS copies;
+// measured on MI355X it is slower (145 us vs 121 us), so the default is 1.
+#define MPATTN_FWD_SPLIT 1
+#endif
 
 // Row sums above this bound (or not finite) send a stage through the fix-up
 // path, which moves the row's reference max. 2^64 keeps every partial sum and
 // accumulator far from fp32 overflow.
 constexpr float kSumHi = 18446744073709551616.0f;
 
-template <typename T, int D, int W, bool ROPE, bool DENSE>
+// SPLIT = 2: two wavefronts per 32-query block, each over half of the keys,
+// merged through LDS at the end; each half streams its keys through its own
+// LDS ring (both halves share the per-stage barrier).
+template <typename T, int D, int W, int SPLIT, int NBUF, bool ROPE, bool DENSE>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(MPATTN_FWD_WAVES)))
 void fwd_kernel(const FwdArgs args) {
     using S = FwdShape<D>;
@@ -191,26 +215,30 @@ void fwd_kernel(const FwdArgs args) {
     typedef typename E::v8 v8;
     typedef typename E::v2 v2;
     typedef short s4 __attribute__((ext_vector_type(4)));
-    constexpr int NBUF = 2;
+    static_assert(NBUF >= 2 && NBUF <= 4, "LDS stages in flight");
+    static_assert(SPLIT == 1 || SPLIT == 2, "key split");
+    constexpr int WQ = W / SPLIT;               // 32-query blocks per workgroup
     constexpr int TOT = 4 * S::NI;              // DMA wave-instructions per full stage
-    constexpr int NJ = (TOT + W - 1) / W;       // per wavefront (the last may be idle)
+    constexpr int NJ = (TOT + WQ - 1) / WQ;     // per wavefront (the last may be idle)
     // With fused RoPE the logit factor scale*log2(e) is folded into Q.
     constexpr bool FOLDED = ROPE;
     const mpattn_fwd_params& p = args.p;
 
-    __shared__ __attribute__((aligned(1024))) char smem[NBUF * S::STAGE];
+    __shared__ __attribute__((aligned(1024))) char smem[SPLIT * NBUF * S::STAGE];
     __shared__ __attribute__((aligned(16))) int scid[W][NBUF][kBN];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
     const int L = p.L, H = p.H, Lp = args.Lp;
-    const int nqb = (L + 32 * W - 1) / (32 * W);
+    const int half = SPLIT == 1 ? 0 : wave / WQ;  // key half of this wavefront
+    const int qw = wave - half * WQ;              // its query block in the workgroup
+    const int nqb = (L + 32 * WQ - 1) / (32 * WQ);
     const int g = xcd_remap(blockIdx.x, gridDim.x);
     const int qb = g % nqb, bh = g / nqb;
     const int b = bh / H, h = bh % H;
-    const int qw0 = qb * 32 * W;  // first query of the workgroup
-    const int q = qw0 + wave * 32 + ql;
+    const int qw0 = qb * 32 * WQ;  // first query of the workgroup
+    const int q = qw0 + qw * 32 + ql;
     const bool qvalid = q < L;
 
     auto base = [&](const mpattn_tensor& t) {
@@ -238,7 +266,7 @@ void fwd_kernel(const FwdArgs args) {
     int dten[NJ];         // tile index, 4 for an idle copy (uniform)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        const int ins0 = wave + j * W;
+        const int ins0 = qw + j * WQ;
         const int ins = ins0 < TOT ? ins0 : TOT - 1;
         const int ten = ins / S::NI, part = ins % S::NI;
         const int slot = part * 64 + lane;
@@ -254,11 +282,12 @@ void fwd_kernel(const FwdArgs args) {
         dloff[j] = r * dstr[j] + cb;
         dten[j] = ins0 < TOT ? ten : 4;
     }
-    const unsigned smem_base = lds_addr(smem);
+    const unsigned smem_base = lds_addr(smem) + half * NBUF * S::STAGE;  // this half's ring
     const unsigned scid_base = lds_addr(&scid[wave][0][0]);
 
     // ---- copy stage s into buffer bf: only the pathways the workgroup needs ----
-    auto issue = [&](int s, int bf, int tiles) {
+    // Returns the number of vector-memory instructions issued (uniform).
+    auto issue = [&](int s, int bf, int tiles) -> int {
         const int k0 = s * kBN;
         const unsigned lb = smem_base + bf * S::STAGE;
         unsigned voff[NJ];
@@ -270,11 +299,16 @@ void fwd_kernel(const FwdArgs args) {
             for (int j = 0; j < NJ; ++j) voff[j] = (unsigned)min(k0 + drow[j], L - 1) * dstr[j] + dcol[j];
         }
         const int m0v = m0_save();
+        int n = 1;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-            if ((tiles >> dten[j]) & 1) dma16(dsb[j], voff[j], lb + dlds[j]);
+            if ((tiles >> dten[j]) & 1) {
+                dma16(dsb[j], voff[j], lb + dlds[j]);
+                ++n;
+            }
         dma4(keff_b, (unsigned)(k0 + lane) * 4u, scid_base + bf * kBN * 4);
         m0_restore(m0v);
+        return n;
     };
 
     // ---- Q fragments (B operand of S^T = K Q^T): dims kk*16 + 8*hh + [0,8) ----
@@ -297,23 +331,27 @@ void fwd_kernel(const FwdArgs args) {
         }
     }
     // Query chain ranges of this wavefront and of the whole workgroup.
-    int cq = 0, cq_min = 0, cq_max = 0, wq_min = 0, wq_max = 0;
+    // (from the per-32-query summaries of the prep kernel: uniform loads)
+    int cq = 0, cq_min = 0, cq_max = 0, wq_min = INT32_MAX, wq_max = INT32_MIN;
     if constexpr (!DENSE) {
         cq = qvalid ? p.chain_id[(int64_t)b * L + q] : 0;
-        cq_min = __builtin_amdgcn_readfirstlane(wave_min_i(qvalid ? cq : INT32_MAX));
-        cq_max = __builtin_amdgcn_readfirstlane(wave_max_i(qvalid ? cq : INT32_MIN));
-        int mn = INT32_MAX, mx = INT32_MIN;
+        const int4* qsum_b = reinterpret_cast<const int4*>(args.qsum) + (int64_t)b * (Lp / 32) + qw0 / 32;
 #pragma unroll
-        for (int r = 0; r < (32 * W + 63) / 64; ++r) {
-            const int qq = qw0 + r * 64 + lane;
-            if (r * 64 + lane < 32 * W && qq < L) {
-                const int c = p.chain_id[(int64_t)b * L + qq];
-                mn = min(mn, c);
-                mx = max(mx, c);
+        for (int w = 0; w < WQ; ++w) {
+            const int4 qs = qsum_b[w < Lp / 32 - qw0 / 32 ? w : 0];
+            if (qw0 + 32 * w < L) {
+                wq_min = min(wq_min, qs.x);
+                wq_max = max(wq_max, qs.y);
+            }
+            if (w == qw) {
+                cq_min = qs.x;
+                cq_max = qs.y;
             }
         }
-        wq_min = __builtin_amdgcn_readfirstlane(wave_min_i(mn));
-        wq_max = __builtin_amdgcn_readfirstlane(wave_max_i(mx));
+        wq_min = __builtin_amdgcn_readfirstlane(wq_min);
+        wq_max = __builtin_amdgcn_readfirstlane(wq_max);
+        cq_min = __builtin_amdgcn_readfirstlane(cq_min);
+        cq_max = __builtin_amdgcn_readfirstlane(cq_max);
     }
     const uint8_t* mrow = nullptr;
     if constexpr (DENSE) {
@@ -644,17 +682,28 @@ void fwd_kernel(const FwdArgs args) {
         return 3;
     };
 
-    // For 64 consecutive 32-key subtiles from kb0: this wavefront's subtile
-    // codes as three bit masks (mb0..mb2 = code bits), and which pathways the
-    // workgroup needs (nS / nM) so stages copy only those tiles.
+    // Subtile codes of this wavefront for the 64 subtiles from kb0, as three
+    // bit masks (mb0..mb2 = code bits), and which pathways the workgroup
+    // needs there (nS / nM) so stages copy only those tiles. Each reload is a
+    // vector load whose wait also drains the copies in flight: windows move
+    // once per 32 stages.
     uint64_t mb0 = 0, mb1 = 0, mb2 = 0, nS = 0, nM = 0;
-    auto load_modes = [&](int kb0) {
+    auto load_codes = [&](int kb0) {
         const int kb = kb0 + lane;
         int code = 4;
-        bool ns = false, nm = false;
         if (kb < Lp / 32) {
             const int4 sm = ksum_b[kb];
             code = subtile_mode(sm.x, sm.y, sm.z);
+        }
+        mb0 = __builtin_amdgcn_ballot_w64(code & 1);
+        mb1 = __builtin_amdgcn_ballot_w64((code >> 1) & 1);
+        mb2 = __builtin_amdgcn_ballot_w64((code >> 2) & 1);
+    };
+    auto load_needs = [&](int kb0) {
+        const int kb = kb0 + lane;
+        bool ns = false, nm = false;
+        if (kb < Lp / 32) {
+            const int4 sm = ksum_b[kb];
             if (sm.z < 32) {
                 if (DENSE || sm.z > 0) {
                     ns = nm = true;
@@ -664,9 +713,6 @@ void fwd_kernel(const FwdArgs args) {
                 }
             }
         }
-        mb0 = __builtin_amdgcn_ballot_w64(code & 1);
-        mb1 = __builtin_amdgcn_ballot_w64((code >> 1) & 1);
-        mb2 = __builtin_amdgcn_ballot_w64((code >> 2) & 1);
         nS = __builtin_amdgcn_ballot_w64(ns);
         nM = __builtin_amdgcn_ballot_w64(nm);
     };
@@ -675,33 +721,65 @@ void fwd_kernel(const FwdArgs args) {
     };
 
     // ---- main loop over stages ----
-    const int nst = (L + kBN - 1) / kBN;
-    int kbase = 0;  // first subtile covered by the masks
-    load_modes(0);  // before any copy is in flight (its wait drains vmcnt)
-    // Tiles a stage copies (bit t = tile t): K_self and V_self (bits 0, 2)
-    // if any subtile needs the self pathway, K_multi and V_multi (1, 3) for
-    // the multimer pathway.
-    auto tiles_of = [&](int nx) -> int {
-        const int t = (((nS >> nx) & 3) != 0 ? 5 : 0) | (((nM >> nx) & 3) != 0 ? 10 : 0);
-        return __builtin_amdgcn_readfirstlane(t);
+    // This wavefront's keys: stages [s_lo, s_lo + s_cnt); both halves run
+    // nloop iterations so the barriers pair up.
+    const int nst_all = (L + kBN - 1) / kBN;
+    const int n0 = SPLIT == 1 ? nst_all : (nst_all + 1) / 2;
+    const int s_lo = half ? n0 : 0;
+    const int s_cnt = half ? nst_all - n0 : n0;
+    const int nloop = n0;
+    int kbp = 2 * s_lo, kbi = 2 * s_lo;  // first subtile of the code / need windows
+    load_codes(kbp);                     // before any copy is in flight
+    load_needs(kbi);
+    // Every prologue load (Q, chain ids, summaries) has landed before the first
+    // copy is issued. The compiler sees this wait (the copies are inline asm it
+    // cannot see), so it adds no vmcnt(0) at later uses, which would also
+    // drain the copies in flight.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // Tiles stage t copies (bit i = tile i): K_self and V_self (bits 0, 2)
+    // if any of its subtiles needs the self pathway, K_multi and V_multi
+    // (1, 3) for the multimer pathway.
+    auto tiles_for = [&](int t) -> int {
+        if (2 * t + 1 - kbi >= 64) {
+            kbi = 2 * t;
+            load_needs(kbi);
+        }
+        const int nx = 2 * t - kbi;
+        const int m = (((nS >> nx) & 3) != 0 ? 5 : 0) | (((nM >> nx) & 3) != 0 ? 10 : 0);
+        return __builtin_amdgcn_readfirstlane(m);
     };
-    issue(0, 0, tiles_of(0));
-    for (int s = 0; s < nst; ++s) {
-        const int bf = s & 1;
-        wait_vm<0>();
+    // pend[k]: vector-memory instructions of local stage s + k still in flight.
+    int pend[NBUF];
+#pragma unroll
+    for (int t = 0; t < NBUF; ++t) pend[t] = 0;
+#pragma unroll
+    for (int t = 0; t < NBUF - 1; ++t)
+        if (t < s_cnt) pend[t] = issue(s_lo + t, t, tiles_for(s_lo + t));
+    int bf = 0;
+    char* const ring = smem + half * NBUF * S::STAGE;
+    for (int s = 0; s < nloop; ++s) {
+        int allow = 0;  // copies of later stages that may stay in flight
+#pragma unroll
+        for (int k = 1; k < NBUF - 1; ++k) allow += pend[k];
+        wait_vm_var(allow);
         stage_barrier();
-        const int sub = 2 * s - kbase;
+#pragma unroll
+        for (int k = 0; k < NBUF - 1; ++k) pend[k] = pend[k + 1];
+        pend[NBUF - 1] = 0;
+        if (s >= s_cnt) continue;  // the shorter half: barrier only
+        const int gs = s_lo + s;   // global stage index
+        if (2 * gs + 1 - kbp >= 64) {
+            kbp = 2 * gs;
+            load_codes(kbp);
+        }
+        const int sub = 2 * gs - kbp;
         const int c0 = code_at(sub), c1 = code_at(sub + 1);
-        if (s + 1 < nst) {
-            if (2 * (s + 1) - kbase >= 64) {  // no copy in flight here
-                kbase = 2 * (s + 1);
-                load_modes(kbase);
-            }
-            const int nx = 2 * (s + 1) - kbase;
-            issue(s + 1, bf ^ 1, tiles_of(nx));
+        if (s + NBUF - 1 < s_cnt) {
+            const int bn = bf + NBUF - 1 >= NBUF ? bf - 1 : bf + NBUF - 1;
+            pend[NBUF - 2] = issue(gs + NBUF - 1, bn, tiles_for(gs + NBUF - 1));
         }
 
-        const char* stage = smem + bf * S::STAGE;
+        const char* stage = ring + bf * S::STAGE;
         bool done = false;
         if (c0 == c1 && c0 <= 1 && !shifted) {
             if (c0 != cur_pw) {  // rare: kept a branch (not selects on every stage)
@@ -714,10 +792,45 @@ void fwd_kernel(const FwdArgs args) {
         }
         if (!done) {
             const int* cid = &scid[wave][bf][0];
-            const int k0 = s * kBN;
+            const int k0 = gs * kBN;
 #pragma unroll 1
             for (int st = 0; st < 2; ++st) slow_subtile(stage, cid, st, st ? c1 : c0, k0);
         }
+        bf = bf + 1 == NBUF ? 0 : bf + 1;
+    }
+
+    // ---- merge the two key halves (SPLIT = 2) ----
+    if constexpr (SPLIT == 2) {
+        // The rings are free once every wavefront passed its last stage.
+        stage_barrier();
+        constexpr int NV = 16 * S::NDB + 2;  // o, l_run, m_ref per lane
+        float* xs = reinterpret_cast<float*>(smem) + (size_t)qw * NV * 64;
+        if (half) {
+#pragma unroll
+            for (int db = 0; db < S::NDB; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) xs[(16 * db + i) * 64 + lane] = o[db][i];
+            xs[(16 * S::NDB) * 64 + lane] = l_run;
+            xs[(16 * S::NDB + 1) * 64 + lane] = m_ref;
+        }
+        stage_barrier();
+        if (half) return;
+        const float lb = xs[(16 * S::NDB) * 64 + lane];
+        const float mb = xs[(16 * S::NDB + 1) * 64 + lane];
+        // A half that accumulated nothing for this query (its sums over both
+        // lane halves are 0) neither sets nor rescales the merged reference.
+        const float laq = l_run + __shfl_xor(l_run, 32);
+        const float lbq = lb + __shfl_xor(lb, 32);
+        float m = m_ref;
+        if (lbq > 0.f) m = laq > 0.f ? fmaxf(m_ref, mb) : mb;
+        const float aa = (laq > 0.f && m_ref != m) ? fast_exp2(m_ref - m) : 1.0f;
+        const float ab = (lbq > 0.f && mb != m) ? fast_exp2(mb - m) : 1.0f;
+#pragma unroll
+        for (int db = 0; db < S::NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[db][i] = o[db][i] * aa + xs[(16 * db + i) * 64 + lane] * ab;
+        l_run = l_run * aa + lb * ab;
+        m_ref = m;
     }
 
     // ---- epilogue: normalise, store O and LSE ----
@@ -747,6 +860,11 @@ void fwd_kernel(const FwdArgs args) {
 template <typename T, int D, bool ROPE, bool DENSE>
 static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     constexpr int W = FwdShape<D>::W;
+    // Optional key split for D <= 32 (see MPATTN_FWD_SPLIT). Two LDS stages per
+    // ring keep two workgroups per CU with the split (D = 64 tiles are twice as
+    // large: two stages, no split).
+    constexpr int SPLIT = D == 64 ? 1 : MPATTN_FWD_SPLIT;
+    constexpr int NBUF = (D == 64 || SPLIT == 2) ? 2 : MPATTN_FWD_NBUF;
     const mpattn_fwd_params& p = a.p;
     const int Lp = round_up(p.L, kBN);
     a.Lp = Lp;
@@ -754,20 +872,24 @@ static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     char* wsb = (char*)p.workspace;
     int* keff = (int*)(wsb + ws.keff);
     int* ksum = (int*)(wsb + ws.ksum);
+    int* qsum = (int*)(wsb + ws.qsum);
     T* krot = (T*)(wsb + ws.krot);
     a.keff = keff;
     a.ksum = ksum;
+    a.qsum = qsum;
     a.krot = krot;
     const int nchain = (p.B * (Lp / 64) + 3) / 4;
     constexpr int NPC = ((D / 2) % 8 == 0) ? D / 16 : 1;
     const int64_t nrot = ROPE ? ((int64_t)p.B * p.H * Lp * NPC + 255) / 256 : 0;
     hipLaunchKernelGGL((fwd_prep_kernel<T, D, ROPE, DENSE>), dim3((unsigned)(nchain + nrot)), dim3(256), 0,
-                       stream, p, keff, ksum, krot, Lp, nchain);
+                       stream, p, keff, ksum, qsum, krot, Lp, nchain);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int nqb = (p.L + 32 * W - 1) / (32 * W);
+    constexpr int WQ = W / SPLIT;
+    const int nqb = (p.L + 32 * WQ - 1) / (32 * WQ);
     const int64_t grid = (int64_t)p.B * p.H * nqb;
-    hipLaunchKernelGGL((fwd_kernel<T, D, W, ROPE, DENSE>), dim3((unsigned)grid), dim3(W * 64), 0, stream, a);
+    hipLaunchKernelGGL((fwd_kernel<T, D, W, SPLIT, NBUF, ROPE, DENSE>), dim3((unsigned)grid), dim3(W * 64), 0,
+                       stream, a);
     return hipGetLastError();
 }
 
