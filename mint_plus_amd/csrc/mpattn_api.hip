@@ -124,7 +124,6 @@ int mpattn_fwd(const mpattn_fwd_params* p, void* stream) {
     if (p->dtype == MPATTN_FP32) {
         e = mpattn::launch_fwd32(*p, (hipStream_t)stream);
     } else {
-        if (p->sqrt_softmax) return fail(MPATTN_ERR_UNSUPPORTED, "sqrt_softmax not built for 16-bit yet");
         e = mpattn::launch_fwd16(*p, (hipStream_t)stream);
     }
     if (e != hipSuccess) return fail(MPATTN_ERR_LAUNCH, "fwd launch: %s", hipGetErrorString(e));

@@ -84,7 +84,8 @@ struct BwdArgs {
     const void* qrot;
     const void* krot;
     int Lp;
-    float c;  // scale * log2(e)
+    float c;     // logit factor: scale * log2(e), halved for sqrt-softmax
+    float lmul;  // LSE factor: log2(e), halved for sqrt-softmax
 };
 
 // ---------------------------------------------------------------------------
@@ -161,7 +162,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* l
             }
             const float lse = p.lse[((int64_t)b * p.H + h) * L + t];
             // A row whose keys are all padded has LSE = -inf and no probabilities.
-            l2 = lse == -INFINITY ? INFINITY : lse * kLog2e;
+            l2 = lse == -INFINITY ? INFINITY : lse * a.lmul;
         }
         lse2[row] = l2;
         delta[row] = dl;
@@ -189,6 +190,16 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* l
             *reinterpret_cast<v8*>(dst + d0) = pack8<T>(x);
         }
     }
+}
+
+// Logit gradient from the recomputed weight w (P, or sqrt(P) for
+// sqrt-softmax), dw = dO . V_sel and delta = dO . O:
+//   softmax:       dS = P (dP - delta)
+//   sqrt-softmax:  dS = W dW / 2 - P delta / 2 = W (dW - W delta) / 2
+template <bool SQRT>
+__device__ __forceinline__ float dscore_t(float w, float dw, float delta) {
+    if constexpr (SQRT) return 0.5f * w * (dw - w * delta);
+    return w * (dw - delta);
 }
 
 // Shapes shared by the two gradient kernels.
@@ -255,7 +266,7 @@ __device__ void store_rows(const f32x16* acc, float* scratch, const mpattn_tenso
 // ---------------------------------------------------------------------------
 // dK / dV: key-stationary.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int W, bool ROPE, bool DENSE>
+template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT>
 __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     using TS = TileShape<D>;
     using BS = BwdShape<D>;
@@ -438,6 +449,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     };
 
     const float c = a.c;
+    auto dscore = [](float w, float dw, float delta) { return dscore_t<SQRT>(w, dw, delta); };
     auto mma_kloop = [&](const v8* aop, const v8* bop) {
         f32x16 acc;
 #pragma unroll
@@ -466,7 +478,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 pm[i] = fast_exp2(fmaf(sv[i], c, -l2[i]));
-                dsm[i] = pm[i] * (dp[i] - dl[i]);
+                dsm[i] = dscore(pm[i], dp[i], dl[i]);
                 same[i] = pw == 0;
             }
         } else {
@@ -501,7 +513,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
                 const float s = sm_ ? ss[i] : sm[i];
                 const float dp = sm_ ? dps[i] : dpm[i];
                 pm[i] = kvalid ? fast_exp2(fmaf(s, c, -l2[i])) : 0.f;
-                dsm[i] = pm[i] * (dp - dl[i]);
+                dsm[i] = dscore(pm[i], dp, dl[i]);
             }
         }
         // dV_pw += P^T dO ; dK_pw += dS^T Q_pw, per 16-query chunk cc
@@ -576,7 +588,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
 // ---------------------------------------------------------------------------
 // dQ: query-stationary.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int W, bool ROPE, bool DENSE>
+template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT>
 __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     using TS = TileShape<D>;
     using BS = BwdShape<D>;
@@ -742,6 +754,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
         return db * 32 + (lane & 31) < D ? r8 : zero8;
     };
     const float c = a.c;
+    auto dscore = [](float w, float dw, float delta) { return dscore_t<SQRT>(w, dw, delta); };
     auto mma_kloop = [&](const v8* aop, const v8* bop) {
         f32x16 acc;
 #pragma unroll
@@ -768,7 +781,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const float pv = fast_exp2(fmaf(sv[i], c, -l2));
-                dsv[i] = pv * (dp[i] - dl);
+                dsv[i] = dscore(pv, dp[i], dl);
                 same[i] = pw == 0;
             }
         } else {
@@ -804,7 +817,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
                     const float s = sm_ ? ss[i] : sm[i];
                     const float dp = sm_ ? dps[i] : dpm[i];
                     const float pv = ck == kPadChain ? 0.f : fast_exp2(fmaf(s, c, -l2));
-                    dsv[i] = pv * (dp - dl);
+                    dsv[i] = dscore(pv, dp, dl);
                 }
             }
         }
@@ -866,14 +879,15 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool ROPE, bool DENSE>
+template <typename T, int D, bool ROPE, bool DENSE, bool SQRT>
 static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     constexpr int W = 4;
     BwdArgs a;
     a.p = p;
     const int Lp = rup(p.L, kBS);
     a.Lp = Lp;
-    a.c = p.scale * kLog2e;
+    a.c = p.scale * kLog2e * (SQRT ? 0.5f : 1.0f);
+    a.lmul = kLog2e * (SQRT ? 0.5f : 1.0f);
     const BwdWs ws = bwd_ws_layout(p.B, p.H, p.L, D, sizeof(T), ROPE);
     char* w = (char*)p.workspace;
     float* lse2 = (float*)(w + ws.lse2);
@@ -901,9 +915,9 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     if (e != hipSuccess) return e;
     const int nb = (p.L + 32 * W - 1) / (32 * W);
     const unsigned grid = (unsigned)((int64_t)p.B * p.H * nb);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, DENSE>), dim3(grid), dim3(W * 64), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, DENSE, SQRT>), dim3(grid), dim3(W * 64), 0, stream, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, DENSE>), dim3(grid), dim3(W * 64), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, DENSE, SQRT>), dim3(grid), dim3(W * 64), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -911,8 +925,12 @@ template <typename T, int D>
 static hipError_t dispatch_bwd_d(const mpattn_bwd_params& p, hipStream_t s) {
     const bool rope = p.rope == MPATTN_ROPE_FUSED;
     const bool dense = p.chain_mask != nullptr;
-    if (rope) return dense ? launch_bwd_t<T, D, true, true>(p, s) : launch_bwd_t<T, D, true, false>(p, s);
-    return dense ? launch_bwd_t<T, D, false, true>(p, s) : launch_bwd_t<T, D, false, false>(p, s);
+    if (p.sqrt_softmax) {
+        if (rope) return dense ? launch_bwd_t<T, D, true, true, true>(p, s) : launch_bwd_t<T, D, true, false, true>(p, s);
+        return dense ? launch_bwd_t<T, D, false, true, true>(p, s) : launch_bwd_t<T, D, false, false, true>(p, s);
+    }
+    if (rope) return dense ? launch_bwd_t<T, D, true, true, false>(p, s) : launch_bwd_t<T, D, true, false, false>(p, s);
+    return dense ? launch_bwd_t<T, D, false, true, false>(p, s) : launch_bwd_t<T, D, false, false, false>(p, s);
 }
 
 template <typename T>
@@ -927,7 +945,7 @@ static hipError_t dispatch_bwd_t(const mpattn_bwd_params& p, hipStream_t s) {
 }
 
 hipError_t launch_bwd(const mpattn_bwd_params& p, hipStream_t stream) {
-    if (p.dtype == MPATTN_FP32 || p.sqrt_softmax) return hipErrorInvalidValue;  // not built
+    if (p.dtype == MPATTN_FP32) return hipErrorInvalidValue;  // not built
     if (p.dtype == MPATTN_BF16) return dispatch_bwd_t<bf16_t>(p, stream);
     return dispatch_bwd_t<fp16_t>(p, stream);
 }

@@ -44,6 +44,10 @@ template <> struct Elt<bf16_t> {
         const v2 one = {(bf16_t)1.0f, (bf16_t)1.0f};
         return __builtin_amdgcn_fdot2_f32_bf16(x, one, acc, false);
     }
+    // acc + x[0]^2 + x[1]^2 in fp32.
+    static __device__ __forceinline__ float sq2(v2 x, float acc) {
+        return __builtin_amdgcn_fdot2_f32_bf16(x, x, acc, false);
+    }
 };
 
 template <> struct Elt<fp16_t> {
@@ -56,6 +60,9 @@ template <> struct Elt<fp16_t> {
     static __device__ __forceinline__ float sum2(v2 x, float acc) {
         const v2 one = {(fp16_t)1.0f, (fp16_t)1.0f};
         return __builtin_amdgcn_fdot2(x, one, acc, false);
+    }
+    static __device__ __forceinline__ float sq2(v2 x, float acc) {
+        return __builtin_amdgcn_fdot2(x, x, acc, false);
     }
 };
 

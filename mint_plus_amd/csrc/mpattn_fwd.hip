@@ -207,7 +207,10 @@ constexpr float kSumHi = 18446744073709551616.0f;
 // SPLIT = 2: two wavefronts per 32-query block, each over half of the keys,
 // merged through LDS at the end; each half streams its keys through its own
 // LDS ring (both halves share the per-stage barrier).
-template <typename T, int D, int W, int SPLIT, int NBUF, bool ROPE, bool DENSE>
+// SQRT: sqrt-softmax, O = sum_j sqrt(P_ij) V_j. The kernel then works with
+// e = exp2(s2 / 2) (the 1/2 is folded into the logit factor), accumulates
+// sum e V and sum e^2, and divides by sqrt(sum e^2) at the end.
+template <typename T, int D, int W, int SPLIT, int NBUF, bool ROPE, bool DENSE, bool SQRT>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(MPATTN_FWD_WAVES)))
 void fwd_kernel(const FwdArgs args) {
     using S = FwdShape<D>;
@@ -428,10 +431,17 @@ void fwd_kernel(const FwdArgs args) {
                 pb[st][cc] = __builtin_shufflevector(__builtin_shufflevector(pr[0], pr[1], 0, 1, 2, 3),
                                                      __builtin_shufflevector(pr[2], pr[3], 0, 1, 2, 3), 0, 1, 2,
                                                      3, 4, 5, 6, 7);
-                ls0 = E::sum2(pr[0], ls0);
-                ls1 = E::sum2(pr[1], ls1);
-                ls0 = E::sum2(pr[2], ls0);
-                ls1 = E::sum2(pr[3], ls1);
+                if constexpr (SQRT) {
+                    ls0 = E::sq2(pr[0], ls0);
+                    ls1 = E::sq2(pr[1], ls1);
+                    ls0 = E::sq2(pr[2], ls0);
+                    ls1 = E::sq2(pr[3], ls1);
+                } else {
+                    ls0 = E::sum2(pr[0], ls0);
+                    ls1 = E::sum2(pr[1], ls1);
+                    ls0 = E::sum2(pr[2], ls0);
+                    ls1 = E::sum2(pr[3], ls1);
+                }
             }
         return ls0 + ls1;
     };
@@ -455,7 +465,7 @@ void fwd_kernel(const FwdArgs args) {
         if (lq > 0.f) m_new = fmaxf(m_ref, ms);
         else m_new = ms > -INFINITY ? ms : m_ref;
         const float alpha = lq > 0.f ? fast_exp2(m_ref - m_new) : 1.0f;
-        l_run *= alpha;
+        l_run *= SQRT ? alpha * alpha : alpha;
 #pragma unroll
         for (int db = 0; db < S::NDB; ++db)
 #pragma unroll
@@ -829,13 +839,13 @@ void fwd_kernel(const FwdArgs args) {
         for (int db = 0; db < S::NDB; ++db)
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[db][i] = o[db][i] * aa + xs[(16 * db + i) * 64 + lane] * ab;
-        l_run = l_run * aa + lb * ab;
+        l_run = SQRT ? l_run * aa * aa + lb * ab * ab : l_run * aa + lb * ab;
         m_ref = m;
     }
 
     // ---- epilogue: normalise, store O and LSE ----
     const float l_tot = l_run + __shfl_xor(l_run, 32);
-    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    const float inv = l_tot > 0.f ? (SQRT ? __frsqrt_rn(l_tot) : 1.0f / l_tot) : 0.f;
     if (qvalid) {
         T* orow = (T*)p.out.ptr + b * p.out.stride_b + h * p.out.stride_h + (int64_t)q * p.out.stride_t;
 #pragma unroll
@@ -852,12 +862,12 @@ void fwd_kernel(const FwdArgs args) {
             }
         if (p.lse && hh == 0) {
             p.lse[((int64_t)b * H + h) * L + q] =
-                l_tot > 0.f ? (m_ref + __log2f(l_tot)) * kLn2 : -INFINITY;
+                l_tot > 0.f ? ((SQRT ? 2.0f * m_ref : m_ref) + __log2f(l_tot)) * kLn2 : -INFINITY;
         }
     }
 }
 
-template <typename T, int D, bool ROPE, bool DENSE>
+template <typename T, int D, bool ROPE, bool DENSE, bool SQRT>
 static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     constexpr int W = FwdShape<D>::W;
     // Optional key split for D <= 32 (see MPATTN_FWD_SPLIT). Two LDS stages per
@@ -888,8 +898,8 @@ static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     constexpr int WQ = W / SPLIT;
     const int nqb = (p.L + 32 * WQ - 1) / (32 * WQ);
     const int64_t grid = (int64_t)p.B * p.H * nqb;
-    hipLaunchKernelGGL((fwd_kernel<T, D, W, SPLIT, NBUF, ROPE, DENSE>), dim3((unsigned)grid), dim3(W * 64), 0,
-                       stream, a);
+    hipLaunchKernelGGL((fwd_kernel<T, D, W, SPLIT, NBUF, ROPE, DENSE, SQRT>), dim3((unsigned)grid),
+                       dim3(W * 64), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -897,8 +907,12 @@ template <typename T, int D>
 static hipError_t dispatch_fwd_d(FwdArgs& a, hipStream_t s) {
     const bool rope = a.p.rope == MPATTN_ROPE_FUSED;
     const bool dense = a.p.chain_mask != nullptr;
-    if (rope) return dense ? launch_fwd<T, D, true, true>(a, s) : launch_fwd<T, D, true, false>(a, s);
-    return dense ? launch_fwd<T, D, false, true>(a, s) : launch_fwd<T, D, false, false>(a, s);
+    if (a.p.sqrt_softmax) {
+        if (rope) return dense ? launch_fwd<T, D, true, true, true>(a, s) : launch_fwd<T, D, true, false, true>(a, s);
+        return dense ? launch_fwd<T, D, false, true, true>(a, s) : launch_fwd<T, D, false, false, true>(a, s);
+    }
+    if (rope) return dense ? launch_fwd<T, D, true, true, false>(a, s) : launch_fwd<T, D, true, false, false>(a, s);
+    return dense ? launch_fwd<T, D, false, true, false>(a, s) : launch_fwd<T, D, false, false, false>(a, s);
 }
 
 template <typename T>
@@ -917,9 +931,11 @@ hipError_t launch_fwd16(const mpattn_fwd_params& p, hipStream_t stream) {
     a.p = p;
     // Fused RoPE folds scale * log2(e) into Q; caller-rotated q keeps its
     // exact values and the factor is applied per logit.
+    // Sqrt-softmax works with exp2 of half the base-2 logit.
     const bool fused = p.rope == MPATTN_ROPE_FUSED;
-    a.qmul = fused ? p.scale * kLog2e : 1.0f;
-    a.c = fused ? 1.0f : p.scale * kLog2e;
+    const float f = p.scale * kLog2e * (p.sqrt_softmax ? 0.5f : 1.0f);
+    a.qmul = fused ? f : 1.0f;
+    a.c = fused ? 1.0f : f;
     if (p.dtype == MPATTN_BF16) return dispatch_fwd_t<bf16_t>(a, stream);
     return dispatch_fwd_t<fp16_t>(a, stream);
 }

@@ -173,3 +173,22 @@ def test_bwd_headline_shape():
             err = (gg[sl].float() - r).abs()
             bound = ATOL16 + RTOL16 * r.abs()
             assert bool((err <= bound).all()), f"sample {b} {name}: max err {err.max().item():.4g}"
+
+
+@pytest.mark.parametrize("D", [16, 32, 64])
+def test_bwd_sqrt_softmax(D):
+    """Gradients of the sqrt-softmax variant (dS = W (dW - W delta) / 2)."""
+    print(f"[bwd sqrt] D={D}", flush=True)
+    m = _mpattn()
+    xs, go, cid, kp = make_inputs(2, 2, 140, D, torch.bfloat16, seed=60 + D)
+    g = [x.to(DEV) for x in xs]
+    grads = m.fused_multi_pathway_attention_bwd(*g, None, go.to(DEV),
+                                                chain_ids=torch.from_numpy(cid).to(DEV),
+                                                key_padding_mask=torch.from_numpy(kp).to(DEV),
+                                                rope=True, scale=D ** -0.5, sqrt_softmax=True)
+    torch.cuda.synchronize()
+    got = [t.float().cpu().numpy().astype(np.float64) for t in grads]
+    a = [x.double().numpy() for x in xs]
+    ref = orc.mpattn_backward(*a, go.double().numpy(), chain_ids=cid, key_pad=kp, rope=True,
+                              scale=D ** -0.5, sqrt_softmax=True)
+    assert_grads(got, ref, f"sqrt D={D}")

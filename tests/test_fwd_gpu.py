@@ -201,3 +201,38 @@ def test_fwd_strided_views():
     host = [t.contiguous() for t in views(qkv_s)] + [t.contiguous() for t in views(qkv_m)]
     ref = oracle_out(host, cid, kp, rope=True, scale=D ** -0.5)
     assert_close16(out.float().cpu().numpy(), ref, "strided")
+
+
+@pytest.mark.parametrize("D", [16, 32, 64])
+def test_fwd_sqrt_softmax(D):
+    """muS sqrt-softmax: O = sum_j sqrt(P_ij) V_j (multi_pathway_attention.py:138-165)."""
+    print(f"[fwd sqrt] D={D}", flush=True)
+    m = _mpattn()
+    xs, cid, kp = make_inputs(2, 2, 150, D, torch.bfloat16, seed=40 + D)
+    g = [x.to(DEV) for x in xs]
+    out, lse = m._lib.mpattn_fwd(*g, chain_ids=torch.from_numpy(cid).to(DEV),
+                                 key_padding_mask=torch.from_numpy(kp).to(DEV), rope=True,
+                                 scale=D ** -0.5, sqrt_softmax=True, need_lse=True)
+    torch.cuda.synchronize()
+    a = [x.double().numpy() for x in xs]
+    ref, lse_ref = orc.mpattn_forward(*a, chain_ids=cid, key_pad=kp, rope=True, scale=D ** -0.5,
+                                      sqrt_softmax=True)
+    assert_close16(out.float().cpu().numpy().astype(np.float64), ref, f"sqrt D={D}")
+    np.testing.assert_allclose(lse.cpu().numpy(), lse_ref, atol=2e-2, rtol=1e-3)
+
+
+def test_fwd_sqrt_softmax_dense_prerotated():
+    """sqrt-softmax with the reference contract (dense mask, pre-rotated q/k)."""
+    print("[fwd sqrt dense]", flush=True)
+    D, L = 32, 130
+    xs, cid, kp = make_inputs(2, 2, L, D, torch.bfloat16, seed=45, pad=False)
+    pre = prerotate(xs, D, D ** -0.5)
+    m = _mpattn()
+    g = [x.to(DEV) for x in pre]
+    c = torch.from_numpy(cid)
+    cm = (c[:, :, None] != c[:, None, :]).to(DEV)
+    out = m.fused_multi_pathway_attention(*g, cm, training=False, sqrt_softmax=True)
+    torch.cuda.synchronize()
+    a = [x.double().numpy() for x in pre]
+    ref, _ = orc.mpattn_forward(*a, chain_ids=cid, rope=False, scale=1.0, sqrt_softmax=True)
+    assert_close16(out.float().cpu().numpy().astype(np.float64), ref, "sqrt dense")
