@@ -114,7 +114,7 @@ int mpattn_fwd(const mpattn_fwd_params* p, void* stream) {
         if ((int64_t)p->L * ts[i]->stride_t * es + 64 * es > 0x7fffffffLL)
             return fail(MPATTN_ERR_UNSUPPORTED, "%s: L * stride_t too large for 32-bit row offsets",
                         names[i]);
-    if (p->dtype != MPATTN_FP32) {
+    {
         const int64_t need = mpattn::fwd_workspace_bytes(p->B, p->H, p->L, p->D, p->dtype, p->rope);
         if (!p->workspace || (uintptr_t)p->workspace % 256 || p->workspace_bytes < need)
             return fail(MPATTN_ERR_INVALID, "workspace: need %lld bytes, 256-byte aligned (got %lld)",

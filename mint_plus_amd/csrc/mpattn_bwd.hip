@@ -950,10 +950,5 @@ hipError_t launch_bwd(const mpattn_bwd_params& p, hipStream_t stream) {
     return dispatch_bwd_t<fp16_t>(p, stream);
 }
 
-hipError_t launch_fwd32(const mpattn_fwd_params& p, hipStream_t stream) {
-    (void)p;
-    (void)stream;
-    return hipErrorInvalidValue;
-}
 
 }  // namespace mpattn

@@ -903,6 +903,28 @@ static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// Chain staging for the fp32 kernel (mpattn_fp32.hip): the prep kernel's
+// chain blocks only (the fp32 kernel rotates K_self while staging it).
+void fwd_ws_offsets(int B, int H, int L, int D, int esize, bool rope, int64_t* keff, int64_t* ksum,
+                    int64_t* qsum) {
+    const FwdWs w = fwd_ws_layout(B, H, L, D, esize, rope);
+    *keff = w.keff;
+    *ksum = w.ksum;
+    *qsum = w.qsum;
+}
+
+hipError_t launch_fwd_prep_f32(const mpattn_fwd_params& p, int* keff, int* ksum, int* qsum, int Lp,
+                               hipStream_t stream) {
+    const int nchain = (p.B * (Lp / 64) + 3) / 4;
+    if (p.chain_mask)
+        hipLaunchKernelGGL((fwd_prep_kernel<float, 16, false, true>), dim3((unsigned)nchain), dim3(256), 0,
+                           stream, p, keff, ksum, qsum, (float*)nullptr, Lp, nchain);
+    else
+        hipLaunchKernelGGL((fwd_prep_kernel<float, 16, false, false>), dim3((unsigned)nchain), dim3(256), 0,
+                           stream, p, keff, ksum, qsum, (float*)nullptr, Lp, nchain);
+    return hipGetLastError();
+}
+
 template <typename T, int D>
 static hipError_t dispatch_fwd_d(FwdArgs& a, hipStream_t s) {
     const bool rope = a.p.rope == MPATTN_ROPE_FUSED;
