@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MPATTN_VERSION 1
+#define MPATTN_VERSION 2
 
 enum {
     MPATTN_OK = 0,
@@ -131,6 +131,49 @@ int64_t mpattn_bwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D);
  * fused_multi_pathway_attention_bwd
  * (mint_plus/models/kernels/multi_pathway_attention_bwd.py:15-59). */
 int mpattn_bwd(const mpattn_bwd_params *p, void *stream);
+
+/* Materialised-logit combine. Logit tensors are (B, H, L, L) views given as
+ * mpattn_tensor with stride_t = query-row stride and unit key stride; they
+ * share the values' dtype. chain_mask (B, L, L) is required (nonzero =
+ * different chains). Any L >= 1; head dim D a multiple of 8, at most 64. */
+typedef struct mpattn_combine_fwd_params {
+    mpattn_tensor intra_logits, inter_logits;  /* pre-softmax, padded = -inf */
+    mpattn_tensor intra_values, inter_values;  /* (B, H, L, D)               */
+    mpattn_tensor out;                         /* (B, H, L, D), written      */
+    float *lse;              /* optional (B,H,L) fp32 log-sum-exp, or NULL  */
+    const uint8_t *chain_mask;
+    int64_t mask_stride_b, mask_stride_q, mask_stride_k;
+    int32_t B, H, L, D;
+    int32_t dtype;
+    float dropout_p;         /* must be 0                                    */
+} mpattn_combine_fwd_params;
+
+typedef struct mpattn_combine_bwd_params {
+    mpattn_tensor intra_logits, inter_logits, intra_values, inter_values;
+    mpattn_tensor grad_out;                    /* dO (B, H, L, D)            */
+    mpattn_tensor d_intra_logits, d_inter_logits;  /* (B, H, L, L), written  */
+    mpattn_tensor d_intra_values, d_inter_values;  /* (B, H, L, D), written  */
+    const uint8_t *chain_mask;
+    int64_t mask_stride_b, mask_stride_q, mask_stride_k;
+    void *workspace;         /* >= mpattn_combine_bwd_workspace_size() bytes,
+                                256-byte aligned                            */
+    int32_t B, H, L, D;
+    int32_t dtype;
+    float dropout_p;         /* must be 0                                    */
+} mpattn_combine_bwd_params;
+
+/* Forward of the combine: O = softmax(where(mask, inter, intra)) split by
+ * pathway times (Vs, Vm). Replaces fused_multimer_combine
+ * (mint_plus/models/kernels/__init__.py:179-242); no power-of-2 limit on L. */
+int mpattn_combine_fwd(const mpattn_combine_fwd_params *p, void *stream);
+
+/* Workspace bytes mpattn_combine_bwd needs (row statistics). */
+int64_t mpattn_combine_bwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D);
+
+/* Backward of the combine: gradients of both logit tensors and both value
+ * tensors, deterministic. Replaces fused_multimer_combine_bwd
+ * (mint_plus/models/kernels/__init__.py:247-286). */
+int mpattn_combine_bwd(const mpattn_combine_bwd_params *p, void *stream);
 
 /* Human-readable message for an MPATTN_ERR_* code, and the detail of the
  * most recent validation failure on the calling thread. */

@@ -9,11 +9,15 @@ applies key padding and one softmax over all keys, and returns
 """
 from . import _lib
 from ._lib import MpattnError, MpattnUnsupported, load_library, rope_tables
-from .kernels import (differentiable_multi_pathway_attention, fused_multi_pathway_attention,
-                      fused_multi_pathway_attention_bwd, fused_multi_pathway_attention_fp16)
+from .kernels import (differentiable_multi_pathway_attention, differentiable_multimer_combine,
+                      fused_multi_pathway_attention, fused_multi_pathway_attention_bwd,
+                      fused_multi_pathway_attention_fp16, fused_multimer_combine,
+                      fused_multimer_combine_bwd, multi_pathway_attention_from_qkv)
 
 __all__ = [
     "MpattnError", "MpattnUnsupported", "load_library", "rope_tables",
     "fused_multi_pathway_attention", "fused_multi_pathway_attention_fp16",
     "fused_multi_pathway_attention_bwd", "differentiable_multi_pathway_attention",
+    "fused_multimer_combine", "fused_multimer_combine_bwd", "differentiable_multimer_combine",
+    "multi_pathway_attention_from_qkv",
 ]

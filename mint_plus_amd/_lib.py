@@ -84,12 +84,47 @@ class BwdParams(ctypes.Structure):
     ]
 
 
+class CombineFwdParams(ctypes.Structure):
+    _fields_ = [
+        ("intra_logits", Tensor4), ("inter_logits", Tensor4),
+        ("intra_values", Tensor4), ("inter_values", Tensor4),
+        ("out", Tensor4),
+        ("lse", ctypes.c_void_p),
+        ("chain_mask", ctypes.c_void_p),
+        ("mask_stride_b", ctypes.c_int64), ("mask_stride_q", ctypes.c_int64),
+        ("mask_stride_k", ctypes.c_int64),
+        ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("L", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("dropout_p", ctypes.c_float),
+    ]
+
+
+class CombineBwdParams(ctypes.Structure):
+    _fields_ = [
+        ("intra_logits", Tensor4), ("inter_logits", Tensor4),
+        ("intra_values", Tensor4), ("inter_values", Tensor4),
+        ("grad_out", Tensor4),
+        ("d_intra_logits", Tensor4), ("d_inter_logits", Tensor4),
+        ("d_intra_values", Tensor4), ("d_inter_values", Tensor4),
+        ("chain_mask", ctypes.c_void_p),
+        ("mask_stride_b", ctypes.c_int64), ("mask_stride_q", ctypes.c_int64),
+        ("mask_stride_k", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p),
+        ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("L", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("dropout_p", ctypes.c_float),
+    ]
+
+
 # Functions declared in include/mpattn.h, with their ctypes signatures.
 EXPORTS = {
     "mpattn_fwd": (ctypes.c_int, [ctypes.POINTER(FwdParams), ctypes.c_void_p]),
     "mpattn_bwd": (ctypes.c_int, [ctypes.POINTER(BwdParams), ctypes.c_void_p]),
     "mpattn_fwd_workspace_size": (ctypes.c_int64, [ctypes.c_int32] * 6),
     "mpattn_bwd_workspace_size": (ctypes.c_int64, [ctypes.c_int32] * 4),
+    "mpattn_combine_fwd": (ctypes.c_int, [ctypes.POINTER(CombineFwdParams), ctypes.c_void_p]),
+    "mpattn_combine_bwd": (ctypes.c_int, [ctypes.POINTER(CombineBwdParams), ctypes.c_void_p]),
+    "mpattn_combine_bwd_workspace_size": (ctypes.c_int64, [ctypes.c_int32] * 4),
     "mpattn_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "mpattn_last_error": (ctypes.c_char_p, []),
     "mpattn_version": (ctypes.c_int, []),
@@ -221,6 +256,17 @@ def _common_checks(tensors, names):
             raise ValueError(f"{n} is on {t.device}, expected {t0.device}")
 
 
+def _check_out(t, shape, like, name):
+    """A caller-provided output must match shape, dtype and device and keep
+    the ABI's row alignment (it is written in place, so it cannot be copied)."""
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if t.dtype != like.dtype or t.device != like.device:
+        raise TypeError(f"{name} must be {like.dtype} on {like.device}")
+    if _aligned(t) is not t:
+        raise ValueError(f"{name}: rows must be 16-byte aligned with unit head-dim stride")
+
+
 def _aligned(t):
     """Return t, or a contiguous copy when its layout breaks the ABI's
     16-byte row alignment rule (strides in 16-byte multiples)."""
@@ -249,6 +295,8 @@ def mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, *, chain_ids=N
     dev = q_self.device
     if out is None:
         out = torch.empty((B, H, L, D), dtype=q_self.dtype, device=dev)
+    else:
+        _check_out(out, (B, H, L, D), q_self, "out")
     lse = torch.empty((B, H, L), dtype=torch.float32, device=dev) if need_lse else None
     p = FwdParams()
     p.q_self, p.k_self, p.v_self, p.q_multi, p.k_multi, p.v_multi = (_t4(t) for t in ins)
@@ -279,8 +327,13 @@ def mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, *, chain_ids=N
 
 def mpattn_bwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, out, lse, grad_out, *,
                chain_ids=None, chain_mask=None, key_padding_mask=None, rope=False, scale=1.0,
-               sqrt_softmax=False):
-    """Launch the backward kernels; returns (dq_s, dk_s, dv_s, dq_m, dk_m, dv_m)."""
+               sqrt_softmax=False, grads=None):
+    """Launch the backward kernels; returns (dq_s, dk_s, dv_s, dq_m, dk_m, dv_m).
+
+    ``grads`` optionally supplies the six (B, H, L, D) output views (any
+    strides the ABI accepts, e.g. slices of one projection-gradient buffer);
+    by default they are allocated contiguous.
+    """
     ins = [q_self, k_self, v_self, q_multi, k_multi, v_multi, out, grad_out]
     names = ["q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi", "out", "grad_out"]
     _common_checks(ins, names)
@@ -290,7 +343,14 @@ def mpattn_bwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, out, lse, grad
     ins = [_aligned(t) for t in ins]
     dev = q_self.device
     lib = load_library()
-    grads = [torch.empty((B, H, L, D), dtype=q_self.dtype, device=dev) for _ in range(6)]
+    if grads is None:
+        grads = [torch.empty((B, H, L, D), dtype=q_self.dtype, device=dev) for _ in range(6)]
+    else:
+        grads = list(grads)
+        if len(grads) != 6:
+            raise ValueError("grads must hold six tensors")
+        for g, n in zip(grads, ("dq_self", "dk_self", "dv_self", "dq_multi", "dk_multi", "dv_multi")):
+            _check_out(g, (B, H, L, D), q_self, n)
     ws_bytes = lib.mpattn_bwd_workspace_size(B, H, L, D)
     if ws_bytes < 0:
         raise MpattnError(MPATTN_ERR_INVALID, "mpattn_bwd_workspace_size", "bad shape")
@@ -317,9 +377,98 @@ def mpattn_bwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, out, lse, grad
     return tuple(grads)
 
 
+def _logits4(t, name, B, H, L):
+    """(B, H, L, L) logits view with unit key stride -> Tensor4 (a copy is
+    made when the key stride is not 1)."""
+    if tuple(t.shape) != (B, H, L, L):
+        raise ValueError(f"{name} must be (B, H, L, L) = {(B, H, L, L)}, got {tuple(t.shape)}")
+    if t.stride(3) != 1:
+        t = t.contiguous()
+    return t, Tensor4(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+def _combine_common(intra_logits, inter_logits, chain_mask, intra_values, inter_values):
+    _common_checks([intra_values, inter_values], ["intra_values", "inter_values"])
+    B, H, L, D = intra_values.shape
+    for t, n in ((intra_logits, "intra_logits"), (inter_logits, "inter_logits")):
+        if t.dtype != intra_values.dtype or t.device != intra_values.device:
+            raise TypeError(f"{n} must be {intra_values.dtype} on {intra_values.device}")
+    if tuple(chain_mask.shape) != (B, L, L):
+        raise ValueError(f"chain_mask must be (B, L, L) = {(B, L, L)}, got {tuple(chain_mask.shape)}")
+    cm = chain_mask.to(intra_values.device)
+    if cm.dtype != torch.bool and cm.dtype != torch.uint8:
+        cm = cm != 0
+    return B, H, L, D, cm
+
+
+def mpattn_combine_fwd(intra_logits, inter_logits, chain_mask, intra_values, inter_values, *,
+                       dropout_p=0.0, need_lse=False):
+    """Launch the materialised-logit combine; returns ``out`` (B, H, L, D)
+    (and the fp32 (B, H, L) log-sum-exp when ``need_lse``)."""
+    B, H, L, D, cm = _combine_common(intra_logits, inter_logits, chain_mask, intra_values,
+                                     inter_values)
+    dev = intra_values.device
+    vs, vm = _aligned(intra_values), _aligned(inter_values)
+    il, til = _logits4(intra_logits, "intra_logits", B, H, L)
+    el, tel = _logits4(inter_logits, "inter_logits", B, H, L)
+    out = torch.empty((B, H, L, D), dtype=vs.dtype, device=dev)
+    lse = torch.empty((B, H, L), dtype=torch.float32, device=dev) if need_lse else None
+    p = CombineFwdParams()
+    p.intra_logits, p.inter_logits = til, tel
+    p.intra_values, p.inter_values, p.out = _t4(vs), _t4(vm), _t4(out)
+    p.lse = lse.data_ptr() if lse is not None else None
+    p.chain_mask = cm.data_ptr()
+    p.mask_stride_b, p.mask_stride_q, p.mask_stride_k = cm.stride()
+    p.B, p.H, p.L, p.D = B, H, L, D
+    p.dtype = _DTYPES[vs.dtype]
+    p.dropout_p = float(dropout_p)
+    rc = load_library().mpattn_combine_fwd(ctypes.byref(p), _stream_handle(dev))
+    _check(rc, "mpattn_combine_fwd")
+    del il, el, vs, vm, cm
+    return (out, lse) if need_lse else out
+
+
+def mpattn_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values, inter_values,
+                       grad_out, *, dropout_p=0.0):
+    """Launch the combine backward; returns (d_intra_logits, d_inter_logits,
+    d_intra_values, d_inter_values) in the inputs' dtype."""
+    B, H, L, D, cm = _combine_common(intra_logits, inter_logits, chain_mask, intra_values,
+                                     inter_values)
+    _common_checks([intra_values, grad_out], ["intra_values", "grad_out"])
+    dev = intra_values.device
+    vs, vm, go = _aligned(intra_values), _aligned(inter_values), _aligned(grad_out)
+    il, til = _logits4(intra_logits, "intra_logits", B, H, L)
+    el, tel = _logits4(inter_logits, "inter_logits", B, H, L)
+    d_il = torch.empty((B, H, L, L), dtype=vs.dtype, device=dev)
+    d_el = torch.empty((B, H, L, L), dtype=vs.dtype, device=dev)
+    d_vs = torch.empty((B, H, L, D), dtype=vs.dtype, device=dev)
+    d_vm = torch.empty((B, H, L, D), dtype=vs.dtype, device=dev)
+    lib = load_library()
+    ws_bytes = lib.mpattn_combine_bwd_workspace_size(B, H, L, D)
+    if ws_bytes < 0:
+        raise MpattnError(MPATTN_ERR_INVALID, "mpattn_combine_bwd_workspace_size", "bad shape")
+    ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device=dev)
+    p = CombineBwdParams()
+    p.intra_logits, p.inter_logits = til, tel
+    p.intra_values, p.inter_values, p.grad_out = _t4(vs), _t4(vm), _t4(go)
+    p.d_intra_logits = Tensor4(d_il.data_ptr(), *d_il.stride()[:3])
+    p.d_inter_logits = Tensor4(d_el.data_ptr(), *d_el.stride()[:3])
+    p.d_intra_values, p.d_inter_values = _t4(d_vs), _t4(d_vm)
+    p.chain_mask = cm.data_ptr()
+    p.mask_stride_b, p.mask_stride_q, p.mask_stride_k = cm.stride()
+    p.workspace = ws.data_ptr()
+    p.B, p.H, p.L, p.D = B, H, L, D
+    p.dtype = _DTYPES[vs.dtype]
+    p.dropout_p = float(dropout_p)
+    rc = lib.mpattn_combine_bwd(ctypes.byref(p), _stream_handle(dev))
+    _check(rc, "mpattn_combine_bwd")
+    del il, el, vs, vm, go, cm, ws
+    return d_il, d_el, d_vs, d_vm
+
+
 def default_scale(D):
     return D ** -0.5 if D > 0 else 1.0
 
 
-__all__ = ["mpattn_fwd", "mpattn_bwd", "load_library", "rope_tables", "version",
+__all__ = ["mpattn_fwd", "mpattn_bwd", "mpattn_combine_fwd", "mpattn_combine_bwd", "load_library", "rope_tables", "version",
            "MpattnError", "MpattnUnsupported", "EXPORTS", "LIB_PATH", "default_scale"]

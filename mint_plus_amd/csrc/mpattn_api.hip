@@ -16,6 +16,9 @@ int64_t fwd_workspace_bytes(int B, int H, int L, int D, int dtype, int rope);
 hipError_t launch_fwd32(const mpattn_fwd_params& p, hipStream_t stream);
 hipError_t launch_bwd(const mpattn_bwd_params& p, hipStream_t stream);
 int64_t bwd_workspace_bytes(int B, int H, int L, int D);
+hipError_t launch_combine_fwd(const mpattn_combine_fwd_params& p, float* lse, hipStream_t stream);
+hipError_t launch_combine_bwd(const mpattn_combine_bwd_params& p, hipStream_t stream);
+int64_t combine_bwd_workspace_bytes(int B, int H, int L);
 }  // namespace mpattn
 
 namespace {
@@ -72,6 +75,23 @@ int check_common(int B, int H, int L, int D, int dtype, int rope, float scale,
     const int64_t nblk = (int64_t)B * H * ((L + 127) / 128);
     if (nblk > 0x7fffffffLL || (int64_t)L * 4 > 0x7fffffffLL)
         return fail(MPATTN_ERR_UNSUPPORTED, "problem too large for one launch");
+    return MPATTN_OK;
+}
+
+// Shape, dtype and mask checks shared by the combine entry points.
+int check_combine(int B, int H, int L, int D, int dtype, const uint8_t* mask, int64_t msb,
+                  int64_t msq, int64_t msk, float dropout_p) {
+    if (B < 1 || H < 1 || L < 1) return fail(MPATTN_ERR_INVALID, "B, H, L must be >= 1 (got %d, %d, %d)", B, H, L);
+    if (dtype != MPATTN_BF16 && dtype != MPATTN_FP16 && dtype != MPATTN_FP32)
+        return fail(MPATTN_ERR_INVALID, "unknown dtype %d", dtype);
+    if (D < 8 || D > 64 || D % 8)
+        return fail(MPATTN_ERR_UNSUPPORTED, "combine: head dim %d not supported (multiple of 8, <= 64)", D);
+    if (!mask) return fail(MPATTN_ERR_INVALID, "chain_mask required");
+    if (msb < 0 || msq < 0 || msk < 0) return fail(MPATTN_ERR_UNSUPPORTED, "chain_mask: negative stride");
+    if (dropout_p != 0.f)
+        return fail(MPATTN_ERR_UNSUPPORTED, "dropout_p must be 0 (got %g)", (double)dropout_p);
+    const int64_t nblk = (int64_t)B * H * ((L + 63) / 64);
+    if (nblk > 0x7fffffffLL) return fail(MPATTN_ERR_UNSUPPORTED, "problem too large for one launch");
     return MPATTN_OK;
 }
 
@@ -163,6 +183,59 @@ int mpattn_bwd(const mpattn_bwd_params* p, void* stream) {
     hipError_t e = mpattn::launch_bwd(*p, (hipStream_t)stream);
     if (e == hipErrorInvalidValue) return fail(MPATTN_ERR_UNSUPPORTED, "bwd: configuration not built");
     if (e != hipSuccess) return fail(MPATTN_ERR_LAUNCH, "bwd launch: %s", hipGetErrorString(e));
+    return MPATTN_OK;
+}
+
+int mpattn_combine_fwd(const mpattn_combine_fwd_params* p, void* stream) {
+    g_last_error[0] = 0;
+    if (!p) return fail(MPATTN_ERR_INVALID, "null params");
+    int rc = check_combine(p->B, p->H, p->L, p->D, p->dtype, p->chain_mask, p->mask_stride_b,
+                           p->mask_stride_q, p->mask_stride_k, p->dropout_p);
+    if (rc) return rc;
+    const int es = elt_size(p->dtype);
+    const mpattn_tensor* ts[5] = {&p->intra_logits, &p->inter_logits, &p->intra_values,
+                                  &p->inter_values, &p->out};
+    const char* names[5] = {"intra_logits", "inter_logits", "intra_values", "inter_values", "out"};
+    for (int i = 2; i < 5; ++i)
+        if ((rc = check_tensor(*ts[i], names[i], es, i == 4))) return rc;
+    for (int i = 0; i < 2; ++i)
+        if (!ts[i]->ptr || ts[i]->stride_b < 0 || ts[i]->stride_h < 0 || ts[i]->stride_t < 0)
+            return fail(MPATTN_ERR_INVALID, "%s: null pointer or negative stride", names[i]);
+    if (p->lse && (uintptr_t)p->lse % 4) return fail(MPATTN_ERR_INVALID, "lse misaligned");
+    hipError_t e = mpattn::launch_combine_fwd(*p, p->lse, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(MPATTN_ERR_LAUNCH, "combine fwd launch: %s", hipGetErrorString(e));
+    return MPATTN_OK;
+}
+
+int64_t mpattn_combine_bwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D) {
+    (void)D;
+    if (B < 1 || H < 1 || L < 1) return -1;
+    return mpattn::combine_bwd_workspace_bytes(B, H, L);
+}
+
+int mpattn_combine_bwd(const mpattn_combine_bwd_params* p, void* stream) {
+    g_last_error[0] = 0;
+    if (!p) return fail(MPATTN_ERR_INVALID, "null params");
+    int rc = check_combine(p->B, p->H, p->L, p->D, p->dtype, p->chain_mask, p->mask_stride_b,
+                           p->mask_stride_q, p->mask_stride_k, p->dropout_p);
+    if (rc) return rc;
+    const int es = elt_size(p->dtype);
+    const mpattn_tensor* vt[5] = {&p->intra_values, &p->inter_values, &p->grad_out,
+                                  &p->d_intra_values, &p->d_inter_values};
+    const char* vn[5] = {"intra_values", "inter_values", "grad_out", "d_intra_values",
+                         "d_inter_values"};
+    for (int i = 0; i < 5; ++i)
+        if ((rc = check_tensor(*vt[i], vn[i], es, i >= 3))) return rc;
+    const mpattn_tensor* lt[4] = {&p->intra_logits, &p->inter_logits, &p->d_intra_logits,
+                                  &p->d_inter_logits};
+    const char* ln[4] = {"intra_logits", "inter_logits", "d_intra_logits", "d_inter_logits"};
+    for (int i = 0; i < 4; ++i)
+        if (!lt[i]->ptr || lt[i]->stride_b < 0 || lt[i]->stride_h < 0 || lt[i]->stride_t < 0)
+            return fail(MPATTN_ERR_INVALID, "%s: null pointer or negative stride", ln[i]);
+    if (!p->workspace || (uintptr_t)p->workspace % 256)
+        return fail(MPATTN_ERR_INVALID, "workspace required (256-byte aligned)");
+    hipError_t e = mpattn::launch_combine_bwd(*p, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(MPATTN_ERR_LAUNCH, "combine bwd launch: %s", hipGetErrorString(e));
     return MPATTN_OK;
 }
 

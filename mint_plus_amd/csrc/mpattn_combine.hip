@@ -1,0 +1,683 @@
+// Materialised-logit combine (forward and backward) on gfx950.
+//
+// Replaces fused_multimer_combine / fused_multimer_combine_bwd
+// (mint_plus/models/kernels/__init__.py:179-242, :247-286): given the two
+// (B, H, L, L) logit tensors a caller already holds (pre-softmax, scaled,
+// padded keys at -inf), the (B, L, L) "different chain" mask and the two
+// (B, H, L, D) value tensors,
+//
+//   s_ij = mask_ij ? inter_ij : intra_ij
+//   P_i  = softmax_j(s_i)                       (fp32; all -inf row -> 0)
+//   O_i  = sum_j P_ij (mask_ij ? Vm_j : Vs_j)
+//
+// Backward: dS_ij = P_ij (dO_i . Vsel_j - Delta_i), Delta_i = dO_i . O_i,
+// split into d_intra / d_inter by the mask; dVs_j = sum_i P_ij [!mask] dO_i,
+// dVm_j likewise.
+//
+// The op streams 2 L^2 logits per (b, h) against O(L D) other data, so it is
+// HBM-bound; the kernels read every logit once per pass with 16-byte loads
+// and keep the P.V products on MFMA so the VALU does only the softmax.
+//
+//   combine_fwd:   one wave per 32 queries, 4 waves per workgroup sharing the
+//                  V tiles in LDS. Lane (query c, half h) holds 8 consecutive
+//                  keys of its row: exactly the B operand (P^T, k = key) of
+//                  the 32x32x16 MFMA, whose accumulator O^T then keeps every
+//                  element of a lane on the lane's own query, so the online
+//                  softmax rescale is a per-lane multiply. The running max is
+//                  lazy: it moves only when a chunk exceeds it by 2^8.
+//                  STATS mode writes (lse, Delta = dO . O) instead of O.
+//   combine_dlogits: query-stationary; dW^T = V dO^T on MFMA (V rows read
+//                  straight into the A operand), then the softmax backward on
+//                  the accumulator's 4x4 key groups; writes both d_logits.
+//   combine_dv:    key-stationary; P tiles are recomputed from the logits and
+//                  transposed through LDS, dV^T = dO^T P on MFMA.
+// fp32 uses the 32x32x2 fp32 MFMA with the same lane-to-query mapping.
+#include <math.h>
+
+#include "mpattn_common.h"
+
+namespace mpattn {
+namespace {
+
+struct CombineArgs {
+    const void *il, *el;              // intra / inter logits
+    int64_t il_sb, il_sh, il_st, el_sb, el_sh, el_st;
+    const void *vs, *vm;              // values
+    int64_t vs_sb, vs_sh, vs_st, vm_sb, vm_sh, vm_st;
+    const uint8_t* mask;
+    int64_t m_sb, m_sq, m_sk;
+    void* out;                        // fwd: O; STATS: unused
+    int64_t o_sb, o_sh, o_st;
+    const void* go;                   // grad_out (STATS / bwd)
+    int64_t g_sb, g_sh, g_st;
+    void *dil, *del;                  // d_intra / d_inter logits
+    int64_t dil_sb, dil_sh, dil_st, del_sb, del_sh, del_st;
+    void *dvs, *dvm;                  // d values
+    int64_t dvs_sb, dvs_sh, dvs_st, dvm_sb, dvm_sh, dvm_st;
+    float *lse, *delta;               // (B*H*L)
+    int B, H, L, D;
+};
+
+constexpr float kLog2eC = 1.4426950408889634f;
+constexpr float kLazy = 8.f;  // log2 headroom before the running max moves
+
+// MFMA operand register of one lane: 8 16-bit elements, or one fp32.
+template <typename T> struct OpT { typedef typename Elt<T>::v8 type; };
+template <> struct OpT<float> { typedef float type; };
+
+template <typename T> struct CT;
+template <> struct CT<bf16_t> { typedef bf16x8 v8; typedef bf16x4 v4; };
+template <> struct CT<fp16_t> { typedef fp16x8 v8; typedef fp16x4 v4; };
+
+// N consecutive logits of `row` at key k as fp32; keys >= L read -inf. VEC:
+// the row start is 16-byte aligned (k is a multiple of N), so full groups
+// use vector loads.
+template <typename T, int N, bool VEC>
+__device__ __forceinline__ void load_logits(const T* row, int k, int L, float out[N]) {
+    if (VEC && k + N <= L) {
+        if constexpr (sizeof(T) == 2) {
+            if constexpr (N == 8) {
+                const typename CT<T>::v8 x = *reinterpret_cast<const typename CT<T>::v8*>(row + k);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) out[j] = (float)x[j];
+            } else {
+                const typename CT<T>::v4 x = *reinterpret_cast<const typename CT<T>::v4*>(row + k);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) out[j] = (float)x[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; j += 4) {
+                const f32x4 x = *reinterpret_cast<const f32x4*>(row + k + j);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) out[j + t] = x[t];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < N; ++j) out[j] = (k + j < L) ? (float)row[k + j] : -INFINITY;
+    }
+}
+
+// Bit j set when mask[k + j] is nonzero (keys >= L read 0). VEC: unit key
+// stride and 8-byte aligned rows.
+template <int N, bool VEC>
+__device__ __forceinline__ unsigned load_mask(const uint8_t* row, int64_t sk, int k, int L) {
+    unsigned bits = 0;
+    if (VEC && k + N <= L) {
+        uint64_t x;
+        if constexpr (N == 8) x = *reinterpret_cast<const uint64_t*>(row + k);
+        else x = *reinterpret_cast<const uint32_t*>(row + k);
+#pragma unroll
+        for (int j = 0; j < N; ++j) bits |= (((x >> (8 * j)) & 0xff) != 0) << j;
+    } else {
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+            if (k + j < L && row[(int64_t)(k + j) * sk]) bits |= 1u << j;
+    }
+    return bits;
+}
+
+// 4 consecutive elements at row[d] as fp32 (d % 4 == 0, d < D, D % 8 == 0).
+template <typename T>
+__device__ __forceinline__ void load4f(const T* row, int d, float out[4]) {
+    if constexpr (sizeof(T) == 2) {
+        const typename CT<T>::v4 x = *reinterpret_cast<const typename CT<T>::v4*>(row + d);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[j] = (float)x[j];
+    } else {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(row + d);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[j] = x[j];
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* row, int d, const float v[4]) {
+    if constexpr (sizeof(T) == 2) {
+        typename CT<T>::v4 x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = (T)v[j];
+        *reinterpret_cast<typename CT<T>::v4*>(row + d) = x;
+    } else {
+        *reinterpret_cast<f32x4*>(row + d) = f32x4{v[0], v[1], v[2], v[3]};
+    }
+}
+
+// 8 elements [d0, d0 + 8) of a 16-bit row as an MFMA operand; dims >= D and
+// invalid rows read 0.
+template <typename T>
+__device__ __forceinline__ typename CT<T>::v8 load8op(const T* row, int d0, int D, bool valid) {
+    typename CT<T>::v8 r;
+    if (valid && d0 < D) {
+        r = *reinterpret_cast<const typename CT<T>::v8*>(row + d0);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = (T)0.f;
+    }
+    return r;
+}
+
+__device__ __forceinline__ void decode_bh(int bh, int H, int& b, int& h) {
+    b = bh / H;
+    h = bh - b * H;
+}
+
+// ---------------------------------------------------------------------------
+// Forward (and the backward's statistics pass).
+// ---------------------------------------------------------------------------
+template <typename T, int ND, bool VEC, bool STATS>
+__global__ __launch_bounds__(256) void combine_fwd_kernel(CombineArgs a) {
+    constexpr int KC = 64;               // keys per LDS stage
+    constexpr int DP = ND * 32;          // head dim padded to the MFMA tile
+    constexpr bool F32 = sizeof(T) == 4;
+    constexpr int VT_RS = KC + 8;        // 16-bit: transposed V rows (one per dim)
+    constexpr int VF_RS = DP + 4;        // fp32: V rows (one per key)
+    constexpr int LDS_ELEMS = F32 ? 2 * KC * VF_RS : 2 * DP * VT_RS;
+    __shared__ __align__(16) T lds[LDS_ELEMS];
+
+    const int L = a.L, D = a.D;
+    const int nqb = (L + 127) / 128;
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = bid / nqb, qb = bid - bh * nqb;
+    int b, h;
+    decode_bh(bh, a.H, b, h);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int col = lane & 31, half = lane >> 5;
+    const int q = qb * 128 + wave * 32 + col;
+    const int qc = min(q, L - 1);
+
+    const T* il_row = (const T*)a.il + b * a.il_sb + h * a.il_sh + (int64_t)qc * a.il_st;
+    const T* el_row = (const T*)a.el + b * a.el_sb + h * a.el_sh + (int64_t)qc * a.el_st;
+    const uint8_t* m_row = a.mask + b * a.m_sb + (int64_t)qc * a.m_sq;
+    const T* vs = (const T*)a.vs + b * a.vs_sb + h * a.vs_sh;
+    const T* vm = (const T*)a.vm + b * a.vm_sb + h * a.vm_sh;
+
+    f32x16 acc[ND];
+#pragma unroll
+    for (int n = 0; n < ND; ++n)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[n][i] = 0.f;
+    float mref = -INFINITY, lsum = 0.f;
+
+    const int nch = D / 8;  // 8-element chunks per value row
+    for (int kc = 0; kc < L; kc += KC) {
+        __syncthreads();
+        // Stage the V tiles of both pathways (rows kc .. kc+KC-1; rows >= L
+        // and dims >= D are zero).
+        for (int c = tid; c < 2 * KC * (DP / 8); c += 256) {
+            const int pw = c / (KC * (DP / 8));
+            const int rem = c - pw * KC * (DP / 8);
+            const int r = rem / (DP / 8), dc = rem - r * (DP / 8);
+            const int key = kc + r;
+            float x[8];
+            if (key < L && dc < nch) {
+                const T* src = (pw ? vm + (int64_t)key * a.vm_st : vs + (int64_t)key * a.vs_st) + dc * 8;
+#pragma unroll
+                for (int j = 0; j < 8; j += 4) load4f<T>(src, j, x + j);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = 0.f;
+            }
+            if constexpr (F32) {
+                float* dst = (float*)lds + pw * KC * VF_RS + r * VF_RS + dc * 8;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dst[j] = x[j];
+            } else {
+                T* dst = lds + pw * DP * VT_RS + (dc * 8) * VT_RS + r;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dst[j * VT_RS] = (T)x[j];
+            }
+        }
+        __syncthreads();
+
+#pragma unroll
+        for (int ks = 0; ks < KC / 16; ++ks) {
+            const int k = kc + ks * 16 + half * 8;
+            float si[8], se[8];
+            load_logits<T, 8, VEC>(il_row, k, L, si);
+            load_logits<T, 8, VEC>(el_row, k, L, se);
+            const unsigned bits = load_mask<8, VEC>(m_row, a.m_sk, k, L);
+            float s[8];
+            float cm = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                s[j] = ((bits >> j) & 1 ? se[j] : si[j]) * kLog2eC;
+                cm = fmaxf(cm, s[j]);
+            }
+            cm = fmaxf(cm, __shfl_xor(cm, 32));
+            if (__any(cm > mref + kLazy)) {
+                const float mn = fmaxf(mref, cm);
+                const float f = (mn == -INFINITY) ? 1.f : fast_exp2(mref - mn);
+#pragma unroll
+                for (int n = 0; n < ND; ++n)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) acc[n][i] *= f;
+                lsum *= f;
+                mref = mn;
+            }
+            const float mu = (mref == -INFINITY) ? 0.f : mref;
+            float pi[8], pe[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float p = fast_exp2(s[j] - mu);
+                lsum += p;
+                const bool x = (bits >> j) & 1;
+                pi[j] = x ? 0.f : p;
+                pe[j] = x ? p : 0.f;
+            }
+            if constexpr (F32) {
+                const float* Vs = (const float*)lds + (ks * 16 + half * 8) * VF_RS + col;
+                const float* Vm = Vs + KC * VF_RS;
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+#pragma unroll
+                    for (int n = 0; n < ND; ++n) {
+                        acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[c * VF_RS + n * 32], pi[c],
+                                                                      acc[n], 0, 0, 0);
+                        acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vm[c * VF_RS + n * 32], pe[c],
+                                                                      acc[n], 0, 0, 0);
+                    }
+            } else {
+                const typename Elt<T>::v8 bi = pack8<T>(pi), be = pack8<T>(pe);
+#pragma unroll
+                for (int n = 0; n < ND; ++n) {
+                    const T* vt = lds + (n * 32 + col) * VT_RS + ks * 16 + half * 8;
+                    const typename Elt<T>::v8 as = *reinterpret_cast<const typename Elt<T>::v8*>(vt);
+                    const typename Elt<T>::v8 am =
+                        *reinterpret_cast<const typename Elt<T>::v8*>(vt + DP * VT_RS);
+                    acc[n] = Elt<T>::mma(as, bi, acc[n]);
+                    acc[n] = Elt<T>::mma(am, be, acc[n]);
+                }
+            }
+        }
+    }
+
+    const float lt = lsum + __shfl_xor(lsum, 32);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    const int64_t row = (int64_t)bh * L + qc;
+    if (a.lse && q < L && half == 0) {
+        const float mu = (mref == -INFINITY) ? 0.f : mref;
+        a.lse[row] = lt > 0.f ? (mu + __log2f(lt)) * kLn2 : -INFINITY;
+    }
+    if constexpr (STATS) {
+        const T* g = (const T*)a.go + b * a.g_sb + h * a.g_sh + (int64_t)qc * a.g_st;
+        float dot = 0.f;
+#pragma unroll
+        for (int n = 0; n < ND; ++n)
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const int d = n * 32 + gi * 8 + half * 4;
+                if (d < D) {
+                    float gg[4];
+                    load4f<T>(g, d, gg);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) dot += gg[r] * acc[n][gi * 4 + r];
+                }
+            }
+        dot = (dot + __shfl_xor(dot, 32)) * inv;
+        if (q < L && half == 0) a.delta[row] = dot;
+    } else {
+        if (q < L) {
+            T* o = (T*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)q * a.o_st;
+#pragma unroll
+            for (int n = 0; n < ND; ++n)
+#pragma unroll
+                for (int gi = 0; gi < 4; ++gi) {
+                    const int d = n * 32 + gi * 8 + half * 4;
+                    if (d < D) {
+                        float v[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) v[r] = acc[n][gi * 4 + r] * inv;
+                        store4<T>(o, d, v);
+                    }
+                }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward: d_logits (query-stationary, 32 keys per step).
+// ---------------------------------------------------------------------------
+template <typename T, int ND, bool VEC>
+__global__ __launch_bounds__(256) void combine_dlogits_kernel(CombineArgs a) {
+    constexpr bool F32 = sizeof(T) == 4;
+    const int L = a.L, D = a.D;
+    const int nqb = (L + 127) / 128;
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = bid / nqb, qb = bid - bh * nqb;
+    int b, h;
+    decode_bh(bh, a.H, b, h);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int col = lane & 31, half = lane >> 5;
+    const int q = qb * 128 + wave * 32 + col;
+    const int qc = min(q, L - 1);
+    const bool qv = q < L;
+
+    const T* il_row = (const T*)a.il + b * a.il_sb + h * a.il_sh + (int64_t)qc * a.il_st;
+    const T* el_row = (const T*)a.el + b * a.el_sb + h * a.el_sh + (int64_t)qc * a.el_st;
+    T* dil_row = (T*)a.dil + b * a.dil_sb + h * a.dil_sh + (int64_t)qc * a.dil_st;
+    T* del_row = (T*)a.del + b * a.del_sb + h * a.del_sh + (int64_t)qc * a.del_st;
+    const uint8_t* m_row = a.mask + b * a.m_sb + (int64_t)qc * a.m_sq;
+    const T* vs = (const T*)a.vs + b * a.vs_sb + h * a.vs_sh;
+    const T* vm = (const T*)a.vm + b * a.vm_sb + h * a.vm_sh;
+    const T* g = (const T*)a.go + b * a.g_sb + h * a.g_sh + (int64_t)qc * a.g_st;
+    const int64_t srow = (int64_t)bh * L + qc;
+    const float lse = a.lse[srow];
+    const bool dead = !(lse > -INFINITY);
+    const float lse2 = dead ? 0.f : lse * kLog2eC;
+    const float delta = a.delta[srow];
+
+    // dO^T operand (k = head dim): 16-bit 16 dims per MFMA step, fp32 2.
+    constexpr int NS16 = ND * 2;
+    typename OpT<T>::type gop[F32 ? ND * 16 : NS16];
+    if constexpr (F32) {
+        // 32x32x2: step c covers dims {2c, 2c+1}; lane half supplies dim 2c + half.
+#pragma unroll
+        for (int c = 0; c < ND * 16; ++c) {
+            const int d = 2 * c + half;
+            gop[c] = (qv && d < D) ? (float)g[d] : 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NS16; ++s) gop[s] = load8op<T>(g, s * 16 + half * 8, D, qv);
+    }
+
+    for (int kc = 0; kc < L; kc += 32) {
+        const int kr = kc + col;  // V row this lane feeds to the A operand
+        const bool kv = kr < L;
+        const T* vsr = vs + (int64_t)min(kr, L - 1) * a.vs_st;
+        const T* vmr = vm + (int64_t)min(kr, L - 1) * a.vm_st;
+        f32x16 ws, wm;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ws[i] = wm[i] = 0.f;
+        if constexpr (F32) {
+#pragma unroll
+            for (int c = 0; c < ND * 16; ++c) {
+                const int d = 2 * c + half;
+                const float xs = (kv && d < D) ? (float)vsr[d] : 0.f;
+                const float xm = (kv && d < D) ? (float)vmr[d] : 0.f;
+                ws = __builtin_amdgcn_mfma_f32_32x32x2f32(xs, gop[c], ws, 0, 0, 0);
+                wm = __builtin_amdgcn_mfma_f32_32x32x2f32(xm, gop[c], wm, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < NS16; ++s) {
+                const int d0 = s * 16 + half * 8;
+                ws = Elt<T>::mma(load8op<T>(vsr, d0, D, kv), gop[s], ws);
+                wm = Elt<T>::mma(load8op<T>(vmr, d0, D, kv), gop[s], wm);
+            }
+        }
+        // Accumulator slot 4*gi + r holds key kc + 8*gi + 4*half + r.
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+            const int k = kc + gi * 8 + half * 4;
+            if (k >= L) continue;
+            float si[4], se[4];
+            load_logits<T, 4, VEC>(il_row, k, L, si);
+            load_logits<T, 4, VEC>(el_row, k, L, se);
+            const unsigned bits = load_mask<4, VEC>(m_row, a.m_sk, k, L);
+            float di[4], de[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool x = (bits >> r) & 1;
+                const float s = x ? se[r] : si[r];
+                const float p = dead ? 0.f : fast_exp2(s * kLog2eC - lse2);
+                const float ds = p * ((x ? wm[gi * 4 + r] : ws[gi * 4 + r]) - delta);
+                di[r] = x ? 0.f : ds;
+                de[r] = x ? ds : 0.f;
+            }
+            if (qv) {
+                if (VEC && k + 4 <= L) {
+                    store4<T>(dil_row, k, di);
+                    store4<T>(del_row, k, de);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (k + r < L) {
+                            dil_row[k + r] = (T)di[r];
+                            del_row[k + r] = (T)de[r];
+                        }
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward: dV (key-stationary, 64 keys per workgroup).
+// ---------------------------------------------------------------------------
+template <typename T, int ND, bool VEC>
+__global__ __launch_bounds__(256) void combine_dv_kernel(CombineArgs a) {
+    constexpr bool F32 = sizeof(T) == 4;
+    constexpr int DP = ND * 32;
+    // 16-bit: P^T [2][64 keys][32 q + 8], dO^T [DP][32 + 8].
+    // fp32:   P   [2][32 q][64 + 4],      dO   [32][DP + 4].
+    constexpr int PT_RS = 40, GT_RS = 40;
+    constexpr int PF_RS = 68, GF_RS = DP + 4;
+    constexpr int P_ELEMS = F32 ? 2 * 32 * PF_RS : 2 * 64 * PT_RS;
+    constexpr int G_ELEMS = F32 ? 32 * GF_RS : DP * GT_RS;
+    __shared__ __align__(16) T lp[P_ELEMS];
+    __shared__ __align__(16) T lg[G_ELEMS];
+
+    const int L = a.L, D = a.D;
+    const int nkb = (L + 63) / 64;
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = bid / nkb, kb = bid - bh * nkb;
+    int b, h;
+    decode_bh(bh, a.H, b, h);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int col = lane & 31, half = lane >> 5;
+    const int pw = wave >> 1, kw = (wave & 1) * 32;
+
+    const T* il = (const T*)a.il + b * a.il_sb + h * a.il_sh;
+    const T* el = (const T*)a.el + b * a.el_sb + h * a.el_sh;
+    const uint8_t* mk = a.mask + b * a.m_sb;
+    const T* g = (const T*)a.go + b * a.g_sb + h * a.g_sh;
+    const float* lse = a.lse + (int64_t)bh * L;
+
+    // Loader role: thread -> (query row tq of the chunk, 8-key group tg).
+    const int tq = tid >> 3, tg = tid & 7;
+    const int k8 = kb * 64 + tg * 8;
+
+    f32x16 acc[ND];
+#pragma unroll
+    for (int n = 0; n < ND; ++n)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[n][i] = 0.f;
+
+    const int nch = D / 8;
+    for (int q0 = 0; q0 < L; q0 += 32) {
+        __syncthreads();
+        {
+            const int qq = q0 + tq;
+            const int qc = min(qq, L - 1);
+            float si[8], se[8];
+            load_logits<T, 8, VEC>(il + (int64_t)qc * a.il_st, k8, L, si);
+            load_logits<T, 8, VEC>(el + (int64_t)qc * a.el_st, k8, L, se);
+            const unsigned bits = load_mask<8, VEC>(mk + (int64_t)qc * a.m_sq, a.m_sk, k8, L);
+            const float l = lse[qc];
+            const bool ok = qq < L && l > -INFINITY;
+            const float l2 = ok ? l * kLog2eC : 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const bool x = (bits >> j) & 1;
+                const float p = ok ? fast_exp2((x ? se[j] : si[j]) * kLog2eC - l2) : 0.f;
+                if constexpr (F32) {
+                    float* P = (float*)lp;
+                    P[tq * PF_RS + tg * 8 + j] = x ? 0.f : p;
+                    P[32 * PF_RS + tq * PF_RS + tg * 8 + j] = x ? p : 0.f;
+                } else {
+                    lp[(tg * 8 + j) * PT_RS + tq] = (T)(x ? 0.f : p);
+                    lp[64 * PT_RS + (tg * 8 + j) * PT_RS + tq] = (T)(x ? p : 0.f);
+                }
+            }
+        }
+        // dO rows q0 .. q0+31 (rows >= L and dims >= D are zero).
+        for (int c = tid; c < 32 * (DP / 8); c += 256) {
+            const int r = c / (DP / 8), dc = c - r * (DP / 8);
+            const int qq = q0 + r;
+            float x[8];
+            if (qq < L && dc < nch) {
+                const T* src = g + (int64_t)qq * a.g_st + dc * 8;
+#pragma unroll
+                for (int j = 0; j < 8; j += 4) load4f<T>(src, j, x + j);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = 0.f;
+            }
+            if constexpr (F32) {
+                float* G = (float*)lg + r * GF_RS + dc * 8;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) G[j] = x[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) lg[(dc * 8 + j) * GT_RS + r] = (T)x[j];
+            }
+        }
+        __syncthreads();
+        if constexpr (F32) {
+            const float* P = (const float*)lp + pw * 32 * PF_RS + kw + col;
+            const float* G = (const float*)lg + col;
+#pragma unroll 4
+            for (int c = 0; c < 16; ++c) {
+                const int qr = 2 * c + half;
+                const float bp = P[qr * PF_RS];
+#pragma unroll
+                for (int n = 0; n < ND; ++n)
+                    acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(G[qr * GF_RS + n * 32], bp, acc[n],
+                                                                  0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const typename Elt<T>::v8 bp = *reinterpret_cast<const typename Elt<T>::v8*>(
+                    lp + pw * 64 * PT_RS + (kw + col) * PT_RS + s * 16 + half * 8);
+#pragma unroll
+                for (int n = 0; n < ND; ++n) {
+                    const typename Elt<T>::v8 ag = *reinterpret_cast<const typename Elt<T>::v8*>(
+                        lg + (n * 32 + col) * GT_RS + s * 16 + half * 8);
+                    acc[n] = Elt<T>::mma(ag, bp, acc[n]);
+                }
+            }
+        }
+    }
+
+    const int key = kb * 64 + kw + col;
+    if (key < L) {
+        T* dv = pw ? (T*)a.dvm + b * a.dvm_sb + h * a.dvm_sh + (int64_t)key * a.dvm_st
+                   : (T*)a.dvs + b * a.dvs_sb + h * a.dvs_sh + (int64_t)key * a.dvs_st;
+#pragma unroll
+        for (int n = 0; n < ND; ++n)
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const int d = n * 32 + gi * 8 + half * 4;
+                if (d < D) {
+                    float v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v[r] = acc[n][gi * 4 + r];
+                    store4<T>(dv, d, v);
+                }
+            }
+    }
+}
+
+template <typename T, int ND, bool VEC>
+hipError_t launch_combine_t(const CombineArgs& a, int mode, hipStream_t st) {
+    const int nqb = (a.L + 127) / 128, nkb = (a.L + 63) / 64;
+    const int bh = a.B * a.H;
+    if (mode == 0) {
+        hipLaunchKernelGGL((combine_fwd_kernel<T, ND, VEC, false>), dim3(bh * nqb), dim3(256), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((combine_fwd_kernel<T, ND, VEC, true>), dim3(bh * nqb), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((combine_dlogits_kernel<T, ND, VEC>), dim3(bh * nqb), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((combine_dv_kernel<T, ND, VEC>), dim3(bh * nkb), dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_combine_d(const CombineArgs& a, bool vec, int mode, hipStream_t st) {
+    if (a.D <= 32) return vec ? launch_combine_t<T, 1, true>(a, mode, st) : launch_combine_t<T, 1, false>(a, mode, st);
+    return vec ? launch_combine_t<T, 2, true>(a, mode, st) : launch_combine_t<T, 2, false>(a, mode, st);
+}
+
+bool aligned_rows(const void* p, int64_t sb, int64_t sh, int64_t st, int es) {
+    const int64_t q = 16 / es;
+    return (uintptr_t)p % 16 == 0 && sb % q == 0 && sh % q == 0 && st % q == 0;
+}
+
+void fill_common(CombineArgs& a, const mpattn_tensor& il, const mpattn_tensor& el,
+                 const mpattn_tensor& vs, const mpattn_tensor& vm, const uint8_t* mask, int64_t msb,
+                 int64_t msq, int64_t msk, int B, int H, int L, int D) {
+    a.il = il.ptr; a.il_sb = il.stride_b; a.il_sh = il.stride_h; a.il_st = il.stride_t;
+    a.el = el.ptr; a.el_sb = el.stride_b; a.el_sh = el.stride_h; a.el_st = el.stride_t;
+    a.vs = vs.ptr; a.vs_sb = vs.stride_b; a.vs_sh = vs.stride_h; a.vs_st = vs.stride_t;
+    a.vm = vm.ptr; a.vm_sb = vm.stride_b; a.vm_sh = vm.stride_h; a.vm_st = vm.stride_t;
+    a.mask = mask; a.m_sb = msb; a.m_sq = msq; a.m_sk = msk;
+    a.B = B; a.H = H; a.L = L; a.D = D;
+}
+
+// Whether the logits and mask admit the vector-load path.
+bool vec_ok(const CombineArgs& a, int es) {
+    const bool lg = aligned_rows(a.il, a.il_sb, a.il_sh, a.il_st, es) &&
+                    aligned_rows(a.el, a.el_sb, a.el_sh, a.el_st, es);
+    const bool mk = a.m_sk == 1 && (uintptr_t)a.mask % 8 == 0 && a.m_sb % 8 == 0 && a.m_sq % 8 == 0;
+    return lg && mk;
+}
+
+}  // namespace
+
+int64_t combine_ws_offset_delta(int B, int H, int L) {
+    return (((int64_t)B * H * L * 4) + 255) / 256 * 256;
+}
+
+int64_t combine_bwd_workspace_bytes(int B, int H, int L) {
+    return 2 * combine_ws_offset_delta(B, H, L);
+}
+
+hipError_t launch_combine_fwd(const mpattn_combine_fwd_params& p, float* lse_buf, hipStream_t st) {
+    CombineArgs a{};
+    fill_common(a, p.intra_logits, p.inter_logits, p.intra_values, p.inter_values, p.chain_mask,
+                p.mask_stride_b, p.mask_stride_q, p.mask_stride_k, p.B, p.H, p.L, p.D);
+    a.out = (void*)p.out.ptr; a.o_sb = p.out.stride_b; a.o_sh = p.out.stride_h; a.o_st = p.out.stride_t;
+    a.lse = lse_buf;
+    const int es = p.dtype == MPATTN_FP32 ? 4 : 2;
+    const bool vec = vec_ok(a, es);
+    switch (p.dtype) {
+        case MPATTN_BF16: return launch_combine_d<bf16_t>(a, vec, 0, st);
+        case MPATTN_FP16: return launch_combine_d<fp16_t>(a, vec, 0, st);
+        default: return launch_combine_d<float>(a, vec, 0, st);
+    }
+}
+
+hipError_t launch_combine_bwd(const mpattn_combine_bwd_params& p, hipStream_t st) {
+    CombineArgs a{};
+    fill_common(a, p.intra_logits, p.inter_logits, p.intra_values, p.inter_values, p.chain_mask,
+                p.mask_stride_b, p.mask_stride_q, p.mask_stride_k, p.B, p.H, p.L, p.D);
+    a.go = p.grad_out.ptr; a.g_sb = p.grad_out.stride_b; a.g_sh = p.grad_out.stride_h;
+    a.g_st = p.grad_out.stride_t;
+    a.dil = (void*)p.d_intra_logits.ptr; a.dil_sb = p.d_intra_logits.stride_b;
+    a.dil_sh = p.d_intra_logits.stride_h; a.dil_st = p.d_intra_logits.stride_t;
+    a.del = (void*)p.d_inter_logits.ptr; a.del_sb = p.d_inter_logits.stride_b;
+    a.del_sh = p.d_inter_logits.stride_h; a.del_st = p.d_inter_logits.stride_t;
+    a.dvs = (void*)p.d_intra_values.ptr; a.dvs_sb = p.d_intra_values.stride_b;
+    a.dvs_sh = p.d_intra_values.stride_h; a.dvs_st = p.d_intra_values.stride_t;
+    a.dvm = (void*)p.d_inter_values.ptr; a.dvm_sb = p.d_inter_values.stride_b;
+    a.dvm_sh = p.d_inter_values.stride_h; a.dvm_st = p.d_inter_values.stride_t;
+    char* ws = (char*)p.workspace;
+    a.lse = (float*)ws;
+    a.delta = (float*)(ws + combine_ws_offset_delta(p.B, p.H, p.L));
+    const int es = p.dtype == MPATTN_FP32 ? 4 : 2;
+    // the d_logits stores use the same vector path as the logit loads
+    const bool vec = vec_ok(a, es) &&
+                     aligned_rows(a.dil, a.dil_sb, a.dil_sh, a.dil_st, es) &&
+                     aligned_rows(a.del, a.del_sb, a.del_sh, a.del_st, es);
+    switch (p.dtype) {
+        case MPATTN_BF16: return launch_combine_d<bf16_t>(a, vec, 1, st);
+        case MPATTN_FP16: return launch_combine_d<fp16_t>(a, vec, 1, st);
+        default: return launch_combine_d<float>(a, vec, 1, st);
+    }
+}
+
+}  // namespace mpattn

@@ -6,10 +6,17 @@ from .multi_pathway_attention import (fused_multi_pathway_attention,
                                       fused_multi_pathway_attention_fp16)
 from .multi_pathway_attention_bwd import fused_multi_pathway_attention_bwd
 from .differentiable_attention import differentiable_multi_pathway_attention
+from .combine import (differentiable_multimer_combine, fused_multimer_combine,
+                      fused_multimer_combine_bwd)
+from .projected import multi_pathway_attention_from_qkv
 
 __all__ = [
     "fused_multi_pathway_attention",
     "fused_multi_pathway_attention_fp16",
     "fused_multi_pathway_attention_bwd",
     "differentiable_multi_pathway_attention",
+    "fused_multimer_combine",
+    "fused_multimer_combine_bwd",
+    "differentiable_multimer_combine",
+    "multi_pathway_attention_from_qkv",
 ]

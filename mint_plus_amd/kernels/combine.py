@@ -1,0 +1,64 @@
+"""Materialised-logit combine on gfx950 (drop-in for
+``mint_plus/models/kernels/__init__.py:179-286`` and
+``mint_plus/models/kernels/differentiable_attention.py:88-140``).
+
+For callers that already hold the two (B, H, T, T) pre-softmax logit tensors:
+``where(chain_mask, inter, intra)`` -> one fp32 softmax over keys -> split by
+pathway -> ``P_intra @ V_self + P_inter @ V_multi``. The kernels behind
+``mpattn_combine_fwd`` / ``mpattn_combine_bwd`` accept any T (no power-of-2
+limit) and bf16, fp16 or fp32 inputs; a row whose keys are all -inf gives 0.
+"""
+import torch
+from torch.autograd import Function
+
+from .. import _lib
+
+
+def _check_mask(chain_mask):
+    if chain_mask.dtype != torch.bool:
+        raise AssertionError("chain_mask must be bool")
+
+
+def fused_multimer_combine(intra_logits, inter_logits, chain_mask, intra_values, inter_values,
+                           dropout_p=0.0):
+    """(B, H, T, D) combined output, ready for ``out_proj``
+    (kernels/__init__.py:179-242). ``dropout_p`` must be 0."""
+    _check_mask(chain_mask)
+    return _lib.mpattn_combine_fwd(intra_logits, inter_logits, chain_mask, intra_values,
+                                   inter_values, dropout_p=dropout_p)
+
+
+def fused_multimer_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values,
+                               inter_values, grad_output, dropout_p=0.0):
+    """(d_intra_logits, d_inter_logits, d_intra_values, d_inter_values) of the
+    combine (kernels/__init__.py:247-286), in the inputs' dtype."""
+    _check_mask(chain_mask)
+    return _lib.mpattn_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values,
+                                   inter_values, grad_output, dropout_p=dropout_p)
+
+
+class _MultimerCombineFn(Function):
+    @staticmethod
+    def forward(ctx, intra_logits, inter_logits, chain_mask, intra_values, inter_values,
+                dropout_p):
+        ctx.save_for_backward(intra_logits, inter_logits, chain_mask, intra_values, inter_values)
+        ctx.dropout_p = dropout_p
+        return fused_multimer_combine(intra_logits, inter_logits, chain_mask, intra_values,
+                                      inter_values, dropout_p=dropout_p)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        il, el, cm, vs, vm = ctx.saved_tensors
+        with torch.no_grad():
+            d_il, d_el, d_vs, d_vm = fused_multimer_combine_bwd(
+                il, el, cm, vs, vm, grad_output.contiguous(), dropout_p=ctx.dropout_p)
+        return d_il, d_el, None, d_vs, d_vm, None
+
+
+def differentiable_multimer_combine(intra_logits, inter_logits, chain_mask, intra_values,
+                                    inter_values, dropout_p=0.0):
+    """``fused_multimer_combine`` with autograd
+    (differentiable_attention.py:127-140)."""
+    _check_mask(chain_mask)
+    return _MultimerCombineFn.apply(intra_logits, inter_logits, chain_mask, intra_values,
+                                    inter_values, float(dropout_p))

@@ -41,6 +41,11 @@ How each function is pinned (``tests/test_oracle.py``):
   appended padded keys, constant V, zero Q), L = 1, and a pure-Python
   triple loop on tiny inputs.
 * ``mpattn_backward``: central finite differences of ``mpattn_forward``.
+* ``combine_forward``: equals ``mpattn_forward`` when fed the logits of the
+  two pathways computed by torch (bmm, scale, -inf padding); all-same-chain
+  reduces to ``torch.softmax(intra) @ Vs``.
+* ``combine_backward``: torch autograd of an independent torch expression
+  and central finite differences of ``combine_forward``.
 """
 import numpy as np
 
@@ -165,6 +170,41 @@ def mpattn_backward(qs, ks, vs, qm, km, vm, grad_out, chain_ids=None, chain_mask
         dq_s = apply_rope_transpose(dq_s, cos, sin)
         dk_s = apply_rope_transpose(dk_s, cos, sin)
     return dq_s, dk_s, dv_s, dq_m, dk_m, dv_m
+
+
+def combine_forward(intra_logits, inter_logits, chain_mask, vs, vm):
+    """Materialised-logit combine in float64: ``where(chain_mask, inter,
+    intra)`` -> one softmax over keys -> split by pathway -> ``P_intra @ Vs +
+    P_inter @ Vm`` (the contract of ``fused_multimer_combine``,
+    ``mint_plus/models/kernels/__init__.py:93-176``, and of the eager
+    ``modules_plus.py:178-194``). Logits already carry the scale and -inf at
+    padded keys; an all -inf row gives 0. Returns ``(out, lse)``."""
+    cross = np.asarray(chain_mask, dtype=bool)
+    il, el = np.asarray(intra_logits, np.float64), np.asarray(inter_logits, np.float64)
+    p, lse = _probs(il, el, cross, None)
+    c = cross[:, None]
+    vs, vm = np.asarray(vs, np.float64), np.asarray(vm, np.float64)
+    out = np.einsum("bhij,bhjd->bhid", np.where(c, 0.0, p), vs) + \
+        np.einsum("bhij,bhjd->bhid", np.where(c, p, 0.0), vm)
+    return out, lse
+
+
+def combine_backward(intra_logits, inter_logits, chain_mask, vs, vm, grad_out):
+    """Gradients (d_intra_logits, d_inter_logits, d_vs, d_vm) of
+    ``sum(grad_out * combine_forward(...)[0])`` in float64 (the contract of
+    ``fused_multimer_combine_bwd``, ``kernels/__init__.py:247-286``)."""
+    cross = np.asarray(chain_mask, dtype=bool)
+    il, el = np.asarray(intra_logits, np.float64), np.asarray(inter_logits, np.float64)
+    vs, vm = np.asarray(vs, np.float64), np.asarray(vm, np.float64)
+    g = np.asarray(grad_out, np.float64)
+    p, _ = _probs(il, el, cross, None)
+    c = cross[:, None]
+    d_vs = np.einsum("bhij,bhid->bhjd", np.where(c, 0.0, p), g)
+    d_vm = np.einsum("bhij,bhid->bhjd", np.where(c, p, 0.0), g)
+    dw = np.where(c, np.einsum("bhid,bhjd->bhij", g, vm), np.einsum("bhid,bhjd->bhij", g, vs))
+    pdp = p * dw
+    ds = pdp - p * pdp.sum(axis=-1, keepdims=True)
+    return np.where(c, 0.0, ds), np.where(c, ds, 0.0), d_vs, d_vm
 
 
 def mpattn_forward_loops(qs, ks, vs, qm, km, vm, chain_ids, key_pad=None, rope=False, scale=1.0):

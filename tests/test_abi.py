@@ -37,7 +37,7 @@ def test_exports_every_header_function(lib):
 
 
 def test_version_and_strings(lib):
-    assert lib.mpattn_version() == 1
+    assert lib.mpattn_version() == 2
     assert lib.mpattn_strerror(0) == b"success"
     assert lib.mpattn_strerror(-2) == b"unsupported configuration"
     assert lib.mpattn_strerror(-99) == b"unknown error"
@@ -154,3 +154,82 @@ def test_python_api_shape_asserts():
         m.fused_multi_pathway_attention(x, y, x, x, x, x, mask, training=False)
     with pytest.raises(AssertionError):
         m.fused_multi_pathway_attention(x, x, x, x, x, x, mask[:, :8], training=False)
+
+
+def _combine_fwd_params(**over):
+    p = _lib.CombineFwdParams()
+    p.intra_logits = p.inter_logits = _lib.Tensor4(1 << 26, 64 * 64 * 20, 64 * 64, 64)
+    for n in ("intra_values", "inter_values", "out"):
+        setattr(p, n, _fake())
+    p.chain_mask = 1 << 21
+    p.mask_stride_b, p.mask_stride_q, p.mask_stride_k = 64 * 64, 64, 1
+    p.B, p.H, p.L, p.D = 2, 20, 64, 32
+    p.dtype = _lib.MPATTN_BF16
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+COMBINE_CASES = [
+    (dict(D=12), _lib.MPATTN_ERR_UNSUPPORTED, "head dim"),
+    (dict(D=72), _lib.MPATTN_ERR_UNSUPPORTED, "head dim"),
+    (dict(B=0), _lib.MPATTN_ERR_INVALID, "must be >= 1"),
+    (dict(dtype=3), _lib.MPATTN_ERR_INVALID, "dtype"),
+    (dict(chain_mask=None), _lib.MPATTN_ERR_INVALID, "chain_mask"),
+    (dict(mask_stride_k=-1), _lib.MPATTN_ERR_UNSUPPORTED, "negative"),
+    (dict(dropout_p=0.1), _lib.MPATTN_ERR_UNSUPPORTED, "dropout"),
+    (dict(intra_logits=_lib.Tensor4(None, 0, 0, 64)), _lib.MPATTN_ERR_INVALID, "intra_logits"),
+    (dict(out=_lib.Tensor4((1 << 20) + 4, 40960, 2048, 32)), _lib.MPATTN_ERR_UNSUPPORTED, "aligned"),
+]
+
+
+@pytest.mark.parametrize("over,code,msg", COMBINE_CASES)
+def test_combine_fwd_validation(lib, over, code, msg):
+    p = _combine_fwd_params(**over)
+    assert lib.mpattn_combine_fwd(ctypes.byref(p), None) == code
+    assert msg in lib.mpattn_last_error().decode()
+
+
+def test_combine_bwd_validation(lib):
+    assert lib.mpattn_combine_bwd(None, None) == _lib.MPATTN_ERR_INVALID
+    p = _lib.CombineBwdParams()
+    lg = _lib.Tensor4(1 << 26, 64 * 64 * 20, 64 * 64, 64)
+    p.intra_logits = p.inter_logits = p.d_intra_logits = p.d_inter_logits = lg
+    for n in ("intra_values", "inter_values", "grad_out", "d_intra_values", "d_inter_values"):
+        setattr(p, n, _fake())
+    p.chain_mask = 1 << 21
+    p.mask_stride_b, p.mask_stride_q, p.mask_stride_k = 64 * 64, 64, 1
+    p.B, p.H, p.L, p.D = 2, 20, 64, 32
+    p.dtype = _lib.MPATTN_FP32
+    # workspace missing
+    assert lib.mpattn_combine_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
+    assert "workspace" in lib.mpattn_last_error().decode()
+    p.workspace = (1 << 24) + 128
+    assert lib.mpattn_combine_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
+    p.workspace = 1 << 24
+    p.dropout_p = 0.5
+    assert lib.mpattn_combine_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_UNSUPPORTED
+
+
+def test_combine_workspace_size(lib):
+    assert lib.mpattn_combine_bwd_workspace_size(0, 1, 1, 32) == -1
+    w = lib.mpattn_combine_bwd_workspace_size(16, 20, 1024, 32)
+    assert w >= 2 * 16 * 20 * 1024 * 4 and w % 256 == 0
+
+
+def test_combine_struct_layout():
+    f = _lib.CombineFwdParams
+    assert f.out.offset == 4 * 32 and f.lse.offset == 5 * 32
+    assert f.B.offset == f.mask_stride_k.offset + 8
+    b = _lib.CombineBwdParams
+    assert b.d_inter_values.offset == 8 * 32 and b.chain_mask.offset == 9 * 32
+    assert b.B.offset == b.workspace.offset + 8
+
+
+def test_combine_python_rejects_non_bool_mask():
+    """As the reference wrapper (kernels/__init__.py:203): the mask must be bool."""
+    import mint_plus_amd as m
+    x = torch.zeros(1, 2, 16, 32)
+    lg = torch.zeros(1, 2, 16, 16)
+    with pytest.raises(AssertionError):
+        m.fused_multimer_combine(lg, lg, torch.zeros(1, 16, 16, dtype=torch.int32), x, x)

@@ -1,0 +1,163 @@
+"""Host-side checks of the module mirrors (CPU, no GPU): constructor and
+parameter names, weight fusion, dispatch flags, helpers, and the eager
+combine path of the layer against the layer oracle."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import two_chain_ids
+from mint_plus_amd import modules as M
+from mint_plus_amd.alphabet import Alphabet
+from mint_plus_amd.attention import MultiHeadAttention, MultimerAttention
+from mint_plus_amd.esm2 import MINT
+from mint_plus_amd.modules_plus import TransformerLayer_MINT_plus, build_mint_plus
+from mint_plus_amd.rotary_embedding import RotaryEmbedding, apply_rotary_pos_emb, rotate_half
+from oracle import model_oracle as mo
+
+
+def test_parameter_names_follow_reference():
+    layer = M.TransformerLayer_MINT(32, 64, 4, use_multimer=True)
+    names = set(dict(layer.named_parameters()))
+    for p in ("self_attn", "multimer_attn"):
+        for n in "qkv":
+            assert f"{p}.{n}_proj.weight" in names and f"{p}.{n}_proj.bias" in names
+    assert "self_attn.out_proj.weight" in names and "multimer_attn.out_proj.weight" not in names
+    assert {"feed_forward.fc1.weight", "feed_forward.fc2.bias", "self_attn_layer_norm.weight",
+            "final_layer_norm.bias"} <= names
+    plus = TransformerLayer_MINT_plus(32, 64, 4, use_multimer=True, use_rmsnorm=True)
+    pn = set(dict(plus.named_parameters()))
+    assert "multimer_attn.fused_qkv.weight" in pn and isinstance(plus.multimer_attn, MultimerAttention)
+    assert isinstance(plus.final_layer_norm, torch.nn.RMSNorm)
+    assert "self_attn.rot_emb.inv_freq" in dict(layer.named_buffers())
+
+
+def test_init_follows_reference():
+    torch.manual_seed(0)
+    a = MultiHeadAttention(64, 4, use_fused_qkv=True)
+    assert torch.all(a.fused_qkv.bias == 0) and torch.all(a.out_proj.bias == 0)
+    bound = 2 ** -0.5 * (6 / (64 + 192)) ** 0.5  # xavier_uniform with gain 2^-1/2
+    assert a.fused_qkv.weight.abs().max() <= bound
+
+
+def test_build_mint_plus_fuses_weights():
+    torch.manual_seed(1)
+    model = MINT(num_layers=2, embed_dim=32, attention_heads=4)
+    model.layers[1]._use_fused_multi_pathway = True
+    old = [dict(l.named_parameters()) for l in model.layers]
+    old = [{k: v.detach().clone() for k, v in d.items()} for d in old]
+    build_mint_plus(model)
+    for i, layer in enumerate(model.layers):
+        assert isinstance(layer, TransformerLayer_MINT_plus)
+        for p in ("self_attn", "multimer_attn"):
+            w = torch.cat([old[i][f"{p}.{n}_proj.weight"] for n in "qkv"])
+            b = torch.cat([old[i][f"{p}.{n}_proj.bias"] for n in "qkv"])
+            mod = getattr(layer, p)
+            assert torch.equal(mod.fused_qkv.weight, w) and torch.equal(mod.fused_qkv.bias, b)
+        assert torch.equal(layer.self_attn.out_proj.weight, old[i]["self_attn.out_proj.weight"])
+        assert torch.equal(layer.feed_forward.fc1.weight, old[i]["feed_forward.fc1.weight"])
+    assert model.layers[1]._use_fused_multi_pathway and not model.layers[0]._use_fused_multi_pathway
+
+
+def test_enable_fused_multi_pathway_reaches_nested_blocks():
+    class Block(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.layers = torch.nn.ModuleList([M.TransformerLayer_MINT(16, 32, 2, use_multimer=True)
+                                               for _ in range(2)])
+
+    class Model(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.layers = torch.nn.ModuleList([Block(), M.TransformerLayer_MINT(16, 32, 2)])
+
+    m = Model()
+    M.enable_fused_multi_pathway(m)
+    assert all(l._use_fused_multi_pathway for l in m.layers[0].layers)
+    assert m.layers[1]._use_fused_multi_pathway
+    M.enable_fused_multi_pathway(m, False)
+    assert not m.layers[1]._use_fused_multi_pathway
+
+
+def test_compute_per_chain_positions():
+    cid = torch.tensor([[0, 0, 0, 1, 1, 1], [0, 1, 1, 2, 2, 2]])
+    ref = torch.tensor([[0, 1, 2, 0, 1, 2], [0, 0, 1, 0, 1, 2]])
+    assert torch.equal(M.compute_per_chain_positions(cid), ref)
+
+
+def test_chain_ids_from_mask_round_trip():
+    rng = np.random.default_rng(0)
+    cid = torch.from_numpy(rng.integers(0, 3, size=(3, 17)))
+    mask = cid[:, :, None] != cid[:, None, :]
+    lab = M.chain_ids_from_mask(mask)
+    assert torch.equal(lab[:, :, None] != lab[:, None, :], mask)
+
+
+def test_alphabet_indices():
+    a = Alphabet.from_architecture("ESM-1b")
+    assert len(a) == 33
+    assert (a.cls_idx, a.padding_idx, a.eos_idx, a.unk_idx, a.mask_idx) == (0, 1, 2, 3, 32)
+    assert a.get_idx("L") == 4 and a.get_idx("C") == 23 and a.get_tok(31) == "<null_1>"
+
+
+def test_rotary_embedding_module():
+    rot = RotaryEmbedding(16)
+    x = torch.randn(3, 10, 16, dtype=torch.float64)
+    y = rot(x)
+    assert y.dtype == x.dtype
+    torch.testing.assert_close(y[:, 0], x[:, 0])                      # position 0
+    torch.testing.assert_close(y.norm(dim=-1), x.norm(dim=-1))        # rotation
+    torch.testing.assert_close(rotate_half(rotate_half(x)), -x)
+    cos, sin = rot.tables(10, x.device, torch.float64)
+    torch.testing.assert_close(apply_rotary_pos_emb(x, cos, sin), y)
+    c32, _ = rot.tables(10, x.device)
+    assert c32.dtype == torch.float32 and rot(x.float()).dtype == torch.float32
+
+
+def test_upgrade_state_dict():
+    m = MINT(num_layers=1, embed_dim=16, attention_heads=2)
+    sd = {"esm.encoder.layer.0.attention.self.query.weight": 1,
+          "esm.encoder.layer.0.attention.output.dense.bias": 2,
+          "esm.encoder.layer.0.intermediate.dense.weight": 3,
+          "esm.encoder.layer.0.output.dense.weight": 4,
+          "esm.encoder.layer.0.LayerNorm.weight": 5,
+          "esm.embeddings.word_embeddings.weight": 6}
+    up = m._upgrade_state_dict(sd)
+    assert up == {"layers.0.self_attn.q_proj.weight": 1, "layers.0.self_attn.out_proj.bias": 2,
+                  "layers.0.feed_forward.fc1.weight": 3, "layers.0.feed_forward.fc2.weight": 4,
+                  "layers.0.final_layer_norm.weight": 5, "embed_tokens.weight": 6}
+
+
+@pytest.mark.parametrize("plus", [False, True])
+def test_eager_combine_path_matches_layer_oracle(plus):
+    """The layer's eager multimer path (torch, CPU float64) equals the layer
+    oracle built from the same state dict."""
+    torch.manual_seed(3)
+    T, B, E, H = 40, 2, 64, 4
+    cls = TransformerLayer_MINT_plus if plus else M.TransformerLayer_MINT
+    layer = cls(E, 2 * E, H, use_multimer=True).double().eval()
+    rng = np.random.default_rng(5)
+    x = torch.from_numpy(rng.standard_normal((T, B, E)))
+    cid = torch.from_numpy(two_chain_ids(rng, B, T))
+    kp = torch.zeros(B, T, dtype=torch.bool)
+    kp[1, -6:] = True
+    with torch.no_grad():
+        h = layer.self_attn_layer_norm(x)
+        att, _ = layer._multimer_attention(h, None, kp, chain_ids=cid)
+        y = x + att
+        y = y + layer.feed_forward(layer.final_layer_norm(y))
+    sd = {"l." + k: v for k, v in layer.state_dict().items()}
+    ref = mo.layer_forward(sd, "l", x, cid.numpy(), kp.numpy(), H)
+    torch.testing.assert_close(y, ref, rtol=0, atol=1e-10)
+
+
+def test_hip_paths_have_no_cpu_fallback():
+    """The fused and combine paths run only in the HIP kernels: CPU tensors
+    are refused."""
+    layer = M.TransformerLayer_MINT(32, 64, 4, use_multimer=True).eval()
+    x = torch.randn(12, 2, 32)
+    cid = torch.zeros(2, 12, dtype=torch.int32)
+    for fused in (True, False):
+        layer._use_fused_multi_pathway = fused
+        with pytest.raises((RuntimeError, AssertionError, ValueError, TypeError)):
+            with torch.no_grad():
+                layer(x, chain_ids=cid)

@@ -1,0 +1,193 @@
+"""Module- and model-level parity on the GPU: ``TransformerLayer_MINT(_plus)``
+and ``MINT`` running the HIP paths (fused multi-pathway kernel, or the
+materialised pipeline with the combine kernel) against the float64 layer /
+model oracle (``oracle/model_oracle.py``) built from the same weights.
+
+Tolerances: fp32 max-abs 1e-4; bf16 |gpu - ref| <= 2e-2 + 1e-2 |ref| (the
+oracle sees the bf16-rounded weights and inputs, so the difference is the
+bf16 arithmetic of the layer).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import two_chain_ids
+from oracle import model_oracle as mo
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _mods():
+    from mint_plus_amd import modules, modules_plus, esm2
+    return modules, modules_plus, esm2
+
+
+def _inputs(T, B, E, seed, dtype, pad=True):
+    rng = np.random.default_rng(seed)
+    x = torch.from_numpy(rng.standard_normal((T, B, E)).astype(np.float32)).to(dtype)
+    cid = torch.from_numpy(two_chain_ids(rng, B, T))
+    kp = torch.zeros(B, T, dtype=torch.bool)
+    if pad:
+        kp[1, T - T // 8:] = True
+    return x, cid, kp
+
+
+def _oracle_layer(layer, x, cid, kp, H):
+    sd = {"l." + k: v for k, v in layer.state_dict().items()}
+    eps = torch.finfo(next(layer.parameters()).dtype).eps
+    return mo.layer_forward(sd, "l", x.double(), cid.numpy(), kp.numpy(), H, norm_eps=eps)
+
+
+def _check(got, ref, dtype, what, valid=None):
+    got = got.double().cpu()
+    if valid is not None:
+        got, ref = got[valid], ref[valid]
+    err = (got - ref).abs()
+    if dtype == torch.float32:
+        assert err.max().item() <= 1e-4, f"{what}: max err {err.max().item():.3g}"
+    else:
+        bad = err > 2e-2 + 1e-2 * ref.abs()
+        assert not bad.any(), f"{what}: {int(bad.sum())} out of tolerance, max {err.max().item():.3g}"
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("plus", [False, True])
+def test_layer_fp32_8m_width(fused, plus):
+    """E=320, H=20 (D=16), fp32: fused kernel path and materialised combine
+    path, base and _plus layers."""
+    print(f"[layer fp32] fused={fused} plus={plus}", flush=True)
+    M, MP, _ = _mods()
+    torch.manual_seed(11)
+    T, B, E, H = 150, 2, 320, 20
+    layer = M.TransformerLayer_MINT(E, 4 * E, H, use_multimer=True)
+    if plus:
+        holder = torch.nn.Module()
+        holder.layers = torch.nn.ModuleList([layer])
+        MP.build_mint_plus(holder)
+        layer = holder.layers[0]
+    layer = layer.to(DEV).eval()
+    layer._use_fused_multi_pathway = fused
+    x, cid, kp = _inputs(T, B, E, 12, torch.float32)
+    with torch.no_grad():
+        y, attn = layer(x.to(DEV), self_attn_padding_mask=kp.to(DEV), chain_ids=cid.to(DEV))
+    torch.cuda.synchronize()
+    assert attn is None
+    _check(y, _oracle_layer(layer, x, cid, kp, H), torch.float32, f"fused={fused} plus={plus}")
+
+
+@pytest.mark.parametrize("E,H", [(640, 20), (480, 20), (1280, 20)])
+def test_layer_bf16_fused(E, H):
+    """bf16 layers of the 150M (D=32), 35M (D=24) and 650M (D=64) widths,
+    fused path, chain selection from the dense (B, T, T) mask."""
+    print(f"[layer bf16] E={E} H={H}", flush=True)
+    M, _, _ = _mods()
+    torch.manual_seed(13)
+    T, B = 200, 2
+    layer = M.TransformerLayer_MINT(E, 4 * E, H, use_multimer=True).to(DEV, torch.bfloat16).eval()
+    layer._use_fused_multi_pathway = True
+    x, cid, kp = _inputs(T, B, E, 14, torch.bfloat16)
+    mask = (cid[:, :, None] != cid[:, None, :]).to(DEV)
+    with torch.no_grad():
+        y, _ = layer(x.to(DEV), self_attn_mask=mask, self_attn_padding_mask=kp.to(DEV))
+    torch.cuda.synchronize()
+    _check(y, _oracle_layer(layer, x, cid, kp, H), torch.bfloat16, f"bf16 E={E}")
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_layer_backward_matches_eager(fused):
+    """Training step through the HIP path (fused kernel bwd, or combine bwd):
+    input and parameter gradients equal those of the eager torch path of the
+    same fp32 layer (relative to each gradient's scale, 1e-4)."""
+    print(f"[layer bwd] fused={fused}", flush=True)
+    M, _, _ = _mods()
+    torch.manual_seed(15)
+    T, B, E, H = 130, 2, 320, 20
+    layer = M.TransformerLayer_MINT(E, 2 * E, H, use_multimer=True).to(DEV).train()
+    x, cid, kp = _inputs(T, B, E, 16, torch.float32)
+    x, cid, kp = x.to(DEV), cid.to(DEV), kp.to(DEV)
+    g = torch.randn(T, B, E, device=DEV, generator=torch.Generator(DEV).manual_seed(1))
+
+    def grads(path):
+        layer.zero_grad(set_to_none=True)
+        xi = x.clone().requires_grad_(True)
+        h = layer.self_attn_layer_norm(xi)
+        if path == "eager":
+            a, _ = layer._multimer_attention(h, None, kp, chain_ids=cid)
+        else:
+            layer._use_fused_multi_pathway = path == "fused"
+            a, _ = layer._multimer_attention_plus(h, None, kp, chain_ids=cid)
+        y = xi + a
+        y = y + layer.feed_forward(layer.final_layer_norm(y))
+        (y * g).sum().backward()
+        out = {"x": xi.grad.clone()}
+        out.update({n: p.grad.clone() for n, p in layer.named_parameters() if p.grad is not None})
+        return out
+
+    got = grads("fused" if fused else "combine")
+    ref = grads("eager")
+    assert set(got) == set(ref)
+    for n in ref:
+        scale = ref[n].abs().max().item()
+        err = (got[n] - ref[n]).abs().max().item()
+        assert err <= 1e-4 * max(scale, 1e-3), f"{n}: err {err:.3g} (scale {scale:.3g})"
+
+
+def _config0_batch(seed=0, B=4):
+    """The 8M configuration's input: two chains A ~ U[60,200], B ~ U[40,160]
+    tokens over the 20 standard amino acids, each wrapped <cls> ... <eos>,
+    laid out [A][B][pad] and padded to the batch max."""
+    from mint_plus_amd.alphabet import Alphabet
+    a = Alphabet.from_architecture("ESM-1b")
+    rng = np.random.default_rng(seed)
+    la = rng.integers(60, 201, size=B)
+    lb = rng.integers(40, 161, size=B)
+    L = int((la + lb).max()) + 4
+    tok = np.full((B, L), a.padding_idx, np.int64)
+    cid = np.ones((B, L), np.int64)
+    for b in range(B):
+        ca = [a.cls_idx] + list(rng.integers(4, 24, size=la[b])) + [a.eos_idx]
+        cb = [a.cls_idx] + list(rng.integers(4, 24, size=lb[b])) + [a.eos_idx]
+        tok[b, :len(ca) + len(cb)] = ca + cb
+        cid[b, :len(ca)] = 0
+    return torch.from_numpy(tok), torch.from_numpy(cid)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_mint_8m_embeddings_fp32(fused):
+    """Config 0: the 8M MINT model in fp32 (random init from a seed), B=4
+    two-chain complexes; per-residue embeddings (final LayerNorm output) at
+    valid positions against the model oracle, max-abs 1e-4."""
+    print(f"[8M model] fused={fused}", flush=True)
+    M, _, E2 = _mods()
+    torch.manual_seed(8)
+    model = E2.MINT.from_config("8M").to(DEV).eval()
+    if fused:
+        M.enable_fused_multi_pathway(model)
+    tok, cid = _config0_batch()
+    with torch.no_grad():
+        res = model(tok.to(DEV), chain_ids=cid.to(DEV), repr_layers=[6])
+    torch.cuda.synchronize()
+    emb = res["representations"][6]
+    sd = {k: v for k, v in model.state_dict().items()}
+    logits_ref, emb_ref = mo.mint_forward(sd, tok, cid, 6, 20)
+    valid = tok != 1
+    _check(emb, emb_ref, torch.float32, "8M embeddings", valid=valid)
+    _check(res["logits"], logits_ref, torch.float32, "8M logits", valid=valid)
+
+
+def test_mint_650m_width_bf16_two_layers():
+    """Two bf16 layers of the 650M width (E=1280, H=20, D=64) inside the MINT
+    trunk, fused path, against the model oracle."""
+    print("[650M-width model]", flush=True)
+    M, _, E2 = _mods()
+    torch.manual_seed(65)
+    model = E2.MINT(num_layers=2, embed_dim=1280, attention_heads=20).to(DEV, torch.bfloat16).eval()
+    M.enable_fused_multi_pathway(model)
+    tok, cid = _config0_batch(seed=3, B=2)
+    with torch.no_grad():
+        res = model(tok.to(DEV), chain_ids=cid.to(DEV), repr_layers=[2])
+    torch.cuda.synchronize()
+    sd = {k: v for k, v in model.state_dict().items()}
+    _, emb_ref = mo.mint_forward(sd, tok, cid, 2, 20, norm_eps=torch.finfo(torch.bfloat16).eps)
+    _check(res["representations"][2], emb_ref, torch.bfloat16, "650M-width", valid=tok != 1)

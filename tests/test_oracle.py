@@ -293,3 +293,90 @@ def test_torch_ref_matches_oracle(dense):
                                dtype=torch.float64, chunk=2, **sel)
     np.testing.assert_allclose(o2.numpy(), out, atol=1e-12)
     np.testing.assert_allclose(l2.numpy(), lse, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# Materialised combine
+# ---------------------------------------------------------------------------
+def _torch_logits(xs, cid, kp, scale):
+    """Both pathways' logits with torch (RoPE by complex multiplication),
+    padded keys at -inf: the inputs fused_multimer_combine receives."""
+    qs, ks, _, qm, km, _ = xs
+    L = qs.shape[2]
+    qr, kr = rope_complex(qs, np.arange(L)), rope_complex(ks, np.arange(L))
+    t = lambda a: torch.as_tensor(np.asarray(a, np.float64))
+    il = scale * torch.matmul(t(qr), t(kr).transpose(-1, -2))
+    el = scale * torch.matmul(t(qm), t(km).transpose(-1, -2))
+    pad = torch.as_tensor(kp)[:, None, None, :]
+    return il.masked_fill(pad, float("-inf")).numpy(), el.masked_fill(pad, float("-inf")).numpy()
+
+
+def test_combine_equals_fused_op_on_torch_logits():
+    rng = np.random.default_rng(60)
+    B, H, L, D = 2, 3, 45, 16
+    xs = rand_inputs(rng, B, H, L, D, sigma=0.8)
+    cid = multi_chain_ids(rng, B, L, 3)
+    kp = tail_padding(rng, B, L, 0.2)
+    kp[1] = True
+    il, el = _torch_logits(xs, cid, kp, 0.4)
+    out, lse = orc.combine_forward(il, el, cid[:, :, None] != cid[:, None, :], xs[2], xs[5])
+    ref, ref_lse = orc.mpattn_forward(*xs, chain_ids=cid, key_pad=kp, rope=True, scale=0.4)
+    np.testing.assert_allclose(out, ref, atol=1e-12)
+    np.testing.assert_allclose(lse, ref_lse, atol=1e-12)
+    assert np.all(out[1] == 0.0)
+
+
+def test_combine_single_chain_is_softmax_of_intra():
+    rng = np.random.default_rng(61)
+    B, H, L, D = 2, 2, 33, 8
+    il, el = rng.standard_normal((2, B, H, L, L))
+    vs, vm = rng.standard_normal((2, B, H, L, D))
+    out, _ = orc.combine_forward(il, el, np.zeros((B, L, L), bool), vs, vm)
+    ref = torch.softmax(torch.as_tensor(il), -1) @ torch.as_tensor(vs)
+    np.testing.assert_allclose(out, ref.numpy(), atol=1e-12)
+    out2, _ = orc.combine_forward(il, el, np.ones((B, L, L), bool), vs, vm)
+    ref2 = torch.softmax(torch.as_tensor(el), -1) @ torch.as_tensor(vm)
+    np.testing.assert_allclose(out2, ref2.numpy(), atol=1e-12)
+
+
+def test_combine_backward_vs_autograd():
+    rng = np.random.default_rng(62)
+    B, H, L, D = 2, 2, 29, 8
+    il, el = rng.standard_normal((2, B, H, L, L)) * 2
+    il[:, :, :, -3:] = -np.inf
+    el[:, :, :, -3:] = -np.inf
+    vs, vm, go = rng.standard_normal((3, B, H, L, D))
+    cm = rng.random((B, L, L)) < 0.4
+    grads = orc.combine_backward(il, el, cm, vs, vm, go)
+    leaves = [torch.as_tensor(a).requires_grad_(True) for a in (il, el, vs, vm)]
+    m = torch.as_tensor(cm)[:, None]
+    p = torch.softmax(torch.where(m, leaves[1], leaves[0]), -1)
+    out = p.masked_fill(m, 0.0) @ leaves[2] + p.masked_fill(~m, 0.0) @ leaves[3]
+    (out * torch.as_tensor(go)).sum().backward()
+    for g, leaf in zip(grads, leaves):
+        ref = torch.nan_to_num(leaf.grad, nan=0.0).numpy()
+        np.testing.assert_allclose(np.nan_to_num(g), ref, atol=1e-12)
+
+
+def test_combine_backward_finite_differences():
+    rng = np.random.default_rng(63)
+    B, H, L, D = 1, 2, 11, 4
+    il, el = rng.standard_normal((2, B, H, L, L))
+    vs, vm, go = rng.standard_normal((3, B, H, L, D))
+    cm = rng.random((B, L, L)) < 0.5
+    grads = orc.combine_backward(il, el, cm, vs, vm, go)
+    args = [il, el, vs, vm]
+
+    def f(a):
+        return float((orc.combine_forward(a[0], a[1], cm, a[2], a[3])[0] * go).sum())
+
+    eps = 1e-6
+    for i in range(4):
+        d = rng.standard_normal(args[i].shape)
+        plus = [x.copy() for x in args]
+        minus = [x.copy() for x in args]
+        plus[i] += eps * d
+        minus[i] -= eps * d
+        fd = (f(plus) - f(minus)) / (2 * eps)
+        an = float((grads[i] * d).sum())
+        assert abs(fd - an) <= 1e-6 * max(1.0, abs(an)), (i, fd, an)
