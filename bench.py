@@ -96,15 +96,67 @@ def cpu_baseline(budget_s=20.0):
                       f"{med * 1e3:.1f} ms/element (full batch ~{med * B:.2f} s)"}
 
 
+def model_batch(device, seed, B, lo, hi, min_chain):
+    """B two-chain complexes of total length ~ U[lo, hi] (each chain >=
+    min_chain tokens) over the 20 standard amino acids (token ids 4..23),
+    laid out [A][B][pad] and padded (id 1) to the batch max."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    lens = [int(torch.randint(lo, hi + 1, (1,), generator=g)) for _ in range(B)]
+    Lm = max(lens)
+    tok = torch.ones(B, Lm, dtype=torch.long)
+    cid = torch.ones(B, Lm, dtype=torch.long)
+    for b, n in enumerate(lens):
+        tok[b, :n] = torch.randint(4, 24, (n,), generator=g)
+        s = int(torch.randint(min_chain, n - min_chain + 1, (1,), generator=g))
+        cid[b, :s] = 0
+    return tok.to(device), cid.to(device)
+
+
+def bench_model(dev, size="650M", dtype=torch.bfloat16, B=8, steps=5, warmup=2,
+                paths=("fused", "combine", "eager")):
+    """Full MINT forward (embedding extraction) with random-init weights:
+    seconds per forward and sequences/s for each multimer-attention path:
+    fused HIP kernel, materialised logits + HIP combine kernel, eager torch."""
+    from mint_plus_amd import esm2, modules
+    torch.manual_seed(65)
+    with torch.device(dev):
+        model = esm2.MINT.from_config(size)
+    model = model.to(dtype).eval()
+    tok, cid = model_batch(dev, 650, B, 512, 1024, 64)
+    stream = torch.cuda.current_stream(dev)
+    out = {"model": size, "B": B, "L_max": int(tok.shape[1]),
+           "tokens": int((tok != 1).sum()), "dtype": str(dtype).replace("torch.", "")}
+    for path in paths:
+        modules.enable_fused_multi_pathway(model, path == "fused")
+        modules.use_eager_multimer(model, path == "eager")
+
+        def step():
+            with torch.inference_mode():
+                model(tok, chain_ids=cid, repr_layers=[model.num_layers])
+
+        _, per = timed(step, steps, warmup, stream)
+        ms = statistics.median(per)
+        out[f"ms_fwd_{path}"] = round(ms, 3)
+        out[f"seqs_per_sec_{path}"] = round(B / (ms * 1e-3), 2)
+    if "fused" in paths and "eager" in paths:
+        out["speedup_fused_vs_eager"] = round(out["ms_fwd_eager"] / out["ms_fwd_fused"], 3)
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--mode", choices=("fwd", "fwdbwd"), default="fwd",
+    ap.add_argument("--mode", choices=("fwd", "fwdbwd", "model", "attn3b"), default="fwd",
                     help="fwd: the headline forward (B=16); fwdbwd: forward + backward at the "
-                         "training shape (B=8, dO ~ N(0, 1))")
+                         "training shape (B=8, dO ~ N(0, 1)); model: 650M MINT forward "
+                         "sequences/s per attention path; attn3b: the op at the 3B shape")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the 650M model forward summary of the default line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="time a plain device copy of MIB MiB instead (HBM counter calibration)")
     args = ap.parse_args()
@@ -136,6 +188,12 @@ def main():
         return
     if args.mode == "fwdbwd":
         return bench_fwdbwd(args, dev)
+    if args.mode == "model":
+        print(json.dumps(bench_model(dev, steps=max(3, min(args.steps, 10)),
+                                     warmup=min(args.warmup, 3))), flush=True)
+        return
+    if args.mode == "attn3b":
+        return bench_attn3b(args, dev)
     xs, cid, pad = make_workload(dev)
     out = torch.empty_like(xs[0])
 
@@ -167,7 +225,7 @@ def main():
     achieved = flops_fwd() / (mean_ms * 1e-3) / 1e12
 
     res = {
-        "metric": "multi-pathway attn fwd TFLOP/s (150M shape, bf16)",
+        "metric": "multi-pathway attn TFLOP/s & % bf16 MFMA peak (150M shape); seqs/sec 650M fwd",
         "value": round(tflops, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -190,6 +248,9 @@ def main():
                      "traffic": measured_traffic("fwd_150m")},
         "cpu_baseline": None,
     }
+    if not args.no_model:
+        # 650M full-model forward, sequences/s: fused HIP path vs eager attention
+        res["model_650m_fwd"] = bench_model(dev, paths=("fused", "eager"))
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)
@@ -274,6 +335,49 @@ def bench_fwdbwd(args, dev):
         "cpu_baseline": None,
     }
     print(json.dumps(res), flush=True)
+
+
+def bench_attn3b(args, dev):
+    """The op at the 3B attention shape: B=4, H=40, D=64, three chains of
+    ~U[200, 800] tokens with L_total <= 2048, padded to 2048."""
+    from mint_plus_amd import _lib
+    b, h, l, d = 4, 40, 2048, 64
+    g = torch.Generator(device="cpu").manual_seed(3000)
+    xs = [(torch.randn(b, h, l, d, generator=g) / d ** 0.5).to(torch.bfloat16).to(dev)
+          for _ in range(6)]
+    cid = torch.full((b, l), 2, dtype=torch.int32)
+    pad = torch.zeros(b, l, dtype=torch.bool)
+    for i in range(b):
+        while True:
+            n = [int(torch.randint(200, 801, (1,), generator=g)) for _ in range(3)]
+            if sum(n) <= l:
+                break
+        cid[i, :n[0]] = 0
+        cid[i, n[0]:n[0] + n[1]] = 1
+        pad[i, sum(n):] = True
+    cid, pad = cid.to(dev), pad.to(dev)
+    out = torch.empty_like(xs[0])
+
+    def step():
+        _lib.mpattn_fwd(*xs, chain_ids=cid, key_padding_mask=pad, rope=True, scale=d ** -0.5,
+                        out=out)
+
+    stream = torch.cuda.current_stream(dev)
+    wall, per = timed(step, args.steps, args.warmup, stream)
+    med = statistics.median(per)
+    fl = 4.0 * b * h * l * l * d
+    print(json.dumps({
+        "metric": "multi-pathway attn fwd TFLOP/s (3B shape, bf16)",
+        "value": round(fl / (med * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 5), "higher_is_better": True,
+        "dtype": "bf16", "data": "synthetic (3 chains ~U[200,800], padded to 2048)",
+        "config": {"workload": "3B-shape multi-pathway attention forward (one layer)",
+                   "B": b, "H": h, "L": l, "D": d, "rope": "fused", "chains": 3},
+        "kernel_ms": {"median": round(med, 5), "p10": round(per[len(per) // 10], 5),
+                      "p90": round(per[(9 * len(per)) // 10], 5)},
+        "pct_bf16_peak": round(100.0 * fl / (med * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+    }), flush=True)
 
 
 if __name__ == "__main__":

@@ -173,6 +173,8 @@ class TransformerLayer_MINT(nn.Module):
         flag is set, else the materialised pipeline with the combine kernel."""
         if self._use_fused_multi_pathway:
             return self._multimer_attention_superfused(x, chain_mask, padding_mask, chain_ids)
+        if getattr(self, "_use_eager_multimer", False):
+            return self._multimer_attention(x, chain_mask, padding_mask, chain_ids)
         T, B, E = x.shape
         sa, ma = self.self_attn, self.multimer_attn
         if chain_mask is None:
@@ -224,3 +226,12 @@ def enable_fused_multi_pathway(model: nn.Module, enabled: bool = True):
     for layer in model.layers:
         for sub in (layer.layers if hasattr(layer, "layers") else (layer,)):
             sub._use_fused_multi_pathway = enabled
+
+
+def use_eager_multimer(model: nn.Module, enabled: bool = True):
+    """Route every layer's non-fused multimer attention through the eager
+    torch combine (``_multimer_attention``, modules.py:94-154) instead of the
+    combine kernel: the baseline the fused path is measured against."""
+    for layer in model.layers:
+        for sub in (layer.layers if hasattr(layer, "layers") else (layer,)):
+            sub._use_eager_multimer = enabled
