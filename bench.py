@@ -151,10 +151,12 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--mode", choices=("fwd", "fwdbwd", "model", "attn3b"), default="fwd",
+    ap.add_argument("--mode", choices=("fwd", "fwdbwd", "model", "attn3b", "combine"),
+                    default="fwd",
                     help="fwd: the headline forward (B=16); fwdbwd: forward + backward at the "
                          "training shape (B=8, dO ~ N(0, 1)); model: 650M MINT forward "
-                         "sequences/s per attention path; attn3b: the op at the 3B shape")
+                         "sequences/s per attention path; attn3b: the op at the 3B shape; "
+                         "combine: the materialised-logit combine fwd and bwd (HBM-bound)")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the 650M model forward summary of the default line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -194,6 +196,8 @@ def main():
         return
     if args.mode == "attn3b":
         return bench_attn3b(args, dev)
+    if args.mode == "combine":
+        return bench_combine(args, dev)
     xs, cid, pad = make_workload(dev)
     out = torch.empty_like(xs[0])
 
@@ -378,6 +382,45 @@ def bench_attn3b(args, dev):
                       "p90": round(per[(9 * len(per)) // 10], 5)},
         "pct_bf16_peak": round(100.0 * fl / (med * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
     }), flush=True)
+
+
+def bench_combine(args, dev, b=8):
+    """fused_multimer_combine (fwd) and fused_multimer_combine_bwd at the
+    150M shape with B=8: two (B, H, L, L) bf16 logit tensors, the (B, L, L)
+    bool mask and two value tensors. Algorithmic bytes: fwd reads 2 logits +
+    mask + 2 values and writes O; bwd reads the same plus dO and writes both
+    d_logits and both d_values (the kernels read the logits three times: the
+    statistics pass, the d_logits pass and the dV pass)."""
+    from mint_plus_amd import _lib
+    g = torch.Generator(device=dev).manual_seed(77)
+    il = (torch.randn(b, H, L, L, device=dev, generator=g) * 2).to(torch.bfloat16)
+    el = (torch.randn(b, H, L, L, device=dev, generator=g) * 2).to(torch.bfloat16)
+    vs = torch.randn(b, H, L, D, device=dev, generator=g).to(torch.bfloat16)
+    vm = torch.randn(b, H, L, D, device=dev, generator=g).to(torch.bfloat16)
+    go = torch.randn(b, H, L, D, device=dev, generator=g).to(torch.bfloat16)
+    _, cid, _ = make_workload(dev)
+    cid = cid[:b]
+    cm = cid[:, :, None] != cid[:, None, :]
+    stream = torch.cuda.current_stream(dev)
+    lg = 2.0 * b * H * L * L * 2
+    vb = b * H * L * D * 2
+    fwd_bytes = lg + b * L * L + 3 * vb
+    bwd_bytes = 2 * lg + b * L * L + 5 * vb  # each input read once, each gradient written once
+    res = {"metric": "materialised combine HBM GB/s (150M shape, B=8, bf16)", "unit": "GB/s",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": "bf16",
+           "data": "synthetic logits N(0,4), 2 chains",
+           "config": {"workload": "fused_multimer_combine fwd / bwd", "B": b, "H": H, "L": L,
+                      "D": D}}
+    for name, fn, nbytes in (
+            ("fwd", lambda: _lib.mpattn_combine_fwd(il, el, cm, vs, vm), fwd_bytes),
+            ("bwd", lambda: _lib.mpattn_combine_bwd(il, el, cm, vs, vm, go), bwd_bytes)):
+        _, per = timed(fn, max(10, args.steps // 4), args.warmup, stream)
+        med = statistics.median(per)
+        res[f"{name}_ms"] = round(med, 4)
+        res[f"{name}_GBs"] = round(nbytes / (med * 1e-3) / 1e9, 1)
+        res[f"{name}_frac_hbm_peak"] = round(nbytes / (med * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+    res["value"] = res["fwd_GBs"]
+    print(json.dumps(res), flush=True)
 
 
 if __name__ == "__main__":
