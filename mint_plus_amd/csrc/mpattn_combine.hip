@@ -26,11 +26,10 @@
 //                  softmax rescale is a per-lane multiply. The running max is
 //                  lazy: it moves only when a chunk exceeds it by 2^8.
 //                  STATS mode writes (lse, Delta = dO . O) instead of O.
-//   combine_dlogits: query-stationary; dW^T = V dO^T on MFMA (V rows read
-//                  straight into the A operand), then the softmax backward on
-//                  the accumulator's 4x4 key groups; writes both d_logits.
-//   combine_dv:    key-stationary; P tiles are recomputed from the logits and
-//                  transposed through LDS, dV^T = dO^T P on MFMA.
+//   combine_bwd:   key-stationary; P tiles are recomputed from coalesced
+//                  logit loads and transposed through LDS, dV^T = dO^T P and
+//                  dW^T = V dO^T on MFMA, then dS = P (dW - Delta) goes out as
+//                  both d_logits with coalesced stores.
 // fp32 uses the 32x32x2 fp32 MFMA with the same lane-to-query mapping.
 #include <math.h>
 
@@ -336,129 +335,48 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(CombineArgs a) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// Backward: d_logits (query-stationary, 32 keys per step).
-// ---------------------------------------------------------------------------
-template <typename T, int ND, bool VEC>
-__global__ __launch_bounds__(256) void combine_dlogits_kernel(CombineArgs a) {
-    constexpr bool F32 = sizeof(T) == 4;
-    const int L = a.L, D = a.D;
-    const int nqb = (L + 127) / 128;
-    const int bid = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = bid / nqb, qb = bid - bh * nqb;
-    int b, h;
-    decode_bh(bh, a.H, b, h);
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int col = lane & 31, half = lane >> 5;
-    const int q = qb * 128 + wave * 32 + col;
-    const int qc = min(q, L - 1);
-    const bool qv = q < L;
-
-    const T* il_row = (const T*)a.il + b * a.il_sb + h * a.il_sh + (int64_t)qc * a.il_st;
-    const T* el_row = (const T*)a.el + b * a.el_sb + h * a.el_sh + (int64_t)qc * a.el_st;
-    T* dil_row = (T*)a.dil + b * a.dil_sb + h * a.dil_sh + (int64_t)qc * a.dil_st;
-    T* del_row = (T*)a.del + b * a.del_sb + h * a.del_sh + (int64_t)qc * a.del_st;
-    const uint8_t* m_row = a.mask + b * a.m_sb + (int64_t)qc * a.m_sq;
-    const T* vs = (const T*)a.vs + b * a.vs_sb + h * a.vs_sh;
-    const T* vm = (const T*)a.vm + b * a.vm_sb + h * a.vm_sh;
-    const T* g = (const T*)a.go + b * a.g_sb + h * a.g_sh + (int64_t)qc * a.g_st;
-    const int64_t srow = (int64_t)bh * L + qc;
-    const float lse = a.lse[srow];
-    const bool dead = !(lse > -INFINITY);
-    const float lse2 = dead ? 0.f : lse * kLog2eC;
-    const float delta = a.delta[srow];
-
-    // dO^T operand (k = head dim): 16-bit 16 dims per MFMA step, fp32 2.
-    constexpr int NS16 = ND * 2;
-    typename OpT<T>::type gop[F32 ? ND * 16 : NS16];
-    if constexpr (F32) {
-        // 32x32x2: step c covers dims {2c, 2c+1}; lane half supplies dim 2c + half.
+// 8 consecutive elements of a row from fp32 values (k % 8 == 0, row 16-byte
+// aligned).
+template <typename T>
+__device__ __forceinline__ void store8(T* row, int k, const float v[8]) {
+    if constexpr (sizeof(T) == 2) {
+        typename CT<T>::v8 x;
 #pragma unroll
-        for (int c = 0; c < ND * 16; ++c) {
-            const int d = 2 * c + half;
-            gop[c] = (qv && d < D) ? (float)g[d] : 0.f;
-        }
+        for (int j = 0; j < 8; ++j) x[j] = (T)v[j];
+        *reinterpret_cast<typename CT<T>::v8*>(row + k) = x;
     } else {
-#pragma unroll
-        for (int s = 0; s < NS16; ++s) gop[s] = load8op<T>(g, s * 16 + half * 8, D, qv);
-    }
-
-    for (int kc = 0; kc < L; kc += 32) {
-        const int kr = kc + col;  // V row this lane feeds to the A operand
-        const bool kv = kr < L;
-        const T* vsr = vs + (int64_t)min(kr, L - 1) * a.vs_st;
-        const T* vmr = vm + (int64_t)min(kr, L - 1) * a.vm_st;
-        f32x16 ws, wm;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) ws[i] = wm[i] = 0.f;
-        if constexpr (F32) {
-#pragma unroll
-            for (int c = 0; c < ND * 16; ++c) {
-                const int d = 2 * c + half;
-                const float xs = (kv && d < D) ? (float)vsr[d] : 0.f;
-                const float xm = (kv && d < D) ? (float)vmr[d] : 0.f;
-                ws = __builtin_amdgcn_mfma_f32_32x32x2f32(xs, gop[c], ws, 0, 0, 0);
-                wm = __builtin_amdgcn_mfma_f32_32x32x2f32(xm, gop[c], wm, 0, 0, 0);
-            }
-        } else {
-#pragma unroll
-            for (int s = 0; s < NS16; ++s) {
-                const int d0 = s * 16 + half * 8;
-                ws = Elt<T>::mma(load8op<T>(vsr, d0, D, kv), gop[s], ws);
-                wm = Elt<T>::mma(load8op<T>(vmr, d0, D, kv), gop[s], wm);
-            }
-        }
-        // Accumulator slot 4*gi + r holds key kc + 8*gi + 4*half + r.
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-            const int k = kc + gi * 8 + half * 4;
-            if (k >= L) continue;
-            float si[4], se[4];
-            load_logits<T, 4, VEC>(il_row, k, L, si);
-            load_logits<T, 4, VEC>(el_row, k, L, se);
-            const unsigned bits = load_mask<4, VEC>(m_row, a.m_sk, k, L);
-            float di[4], de[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const bool x = (bits >> r) & 1;
-                const float s = x ? se[r] : si[r];
-                const float p = dead ? 0.f : fast_exp2(s * kLog2eC - lse2);
-                const float ds = p * ((x ? wm[gi * 4 + r] : ws[gi * 4 + r]) - delta);
-                di[r] = x ? 0.f : ds;
-                de[r] = x ? ds : 0.f;
-            }
-            if (qv) {
-                if (VEC && k + 4 <= L) {
-                    store4<T>(dil_row, k, di);
-                    store4<T>(del_row, k, de);
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        if (k + r < L) {
-                            dil_row[k + r] = (T)di[r];
-                            del_row[k + r] = (T)de[r];
-                        }
-                }
-            }
-        }
+        *reinterpret_cast<f32x4*>(row + k) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(row + k + 4) = f32x4{v[4], v[5], v[6], v[7]};
     }
 }
 
 // ---------------------------------------------------------------------------
-// Backward: dV (key-stationary, 64 keys per workgroup).
+// Backward: dV and both d_logits (key-stationary, 64 keys per workgroup).
+//
+// Per 32-query chunk: every thread loads 8 consecutive keys of one query row
+// of both logit tensors (16-byte loads, 8 threads per 128-byte row segment)
+// and turns them into P with the row's LSE; P^T and the dO tile go to LDS.
+// Wavefront (pathway pw, key half kw) then accumulates dV_pw^T += dO^T P_pw
+// over the chunk and computes dW_pw^T = V_pw dO^T for its 32 keys (V rows held
+// in registers for the whole kernel), written to LDS as fp32. Each thread
+// finally reads dW of its own 8 keys for the selected pathway and writes
+// dS = P (dW - Delta) into d_intra or d_inter with coalesced 16-byte stores.
 // ---------------------------------------------------------------------------
 template <typename T, int ND, bool VEC>
-__global__ __launch_bounds__(256) void combine_dv_kernel(CombineArgs a) {
+__global__ __launch_bounds__(256) void combine_bwd_kernel(CombineArgs a) {
     constexpr bool F32 = sizeof(T) == 4;
     constexpr int DP = ND * 32;
-    // 16-bit: P^T [2][64 keys][32 q + 8], dO^T [DP][32 + 8].
-    // fp32:   P   [2][32 q][64 + 4],      dO   [32][DP + 4].
-    constexpr int PT_RS = 40, GT_RS = 40;
-    constexpr int PF_RS = 68, GF_RS = DP + 4;
+    // 16-bit: P^T [2][64 keys][32 q + 8], dO^T [DP][32 + 8], dO rows [32][DP + 8].
+    // fp32:   P   [2][32 q][64 + 4],      dO rows [32][DP + 4].
+    // both:   dW  fp32 [2][32 q][64 + 4].
+    constexpr int PT_RS = 40, GT_RS = 40, GR_RS = DP + 8;
+    constexpr int PF_RS = 68, GF_RS = DP + 4, W_RS = 68;
     constexpr int P_ELEMS = F32 ? 2 * 32 * PF_RS : 2 * 64 * PT_RS;
-    constexpr int G_ELEMS = F32 ? 32 * GF_RS : DP * GT_RS;
+    constexpr int G_ELEMS = F32 ? 32 * GF_RS : DP * GT_RS + 32 * GR_RS;
     __shared__ __align__(16) T lp[P_ELEMS];
     __shared__ __align__(16) T lg[G_ELEMS];
+    __shared__ __align__(16) float lw[2 * 32 * W_RS];
+    T* lgr = lg + (F32 ? 0 : DP * GT_RS);  // dO rows
 
     const int L = a.L, D = a.D;
     const int nkb = (L + 63) / 64;
@@ -472,9 +390,30 @@ __global__ __launch_bounds__(256) void combine_dv_kernel(CombineArgs a) {
 
     const T* il = (const T*)a.il + b * a.il_sb + h * a.il_sh;
     const T* el = (const T*)a.el + b * a.el_sb + h * a.el_sh;
+    T* dil = (T*)a.dil + b * a.dil_sb + h * a.dil_sh;
+    T* del = (T*)a.del + b * a.del_sb + h * a.del_sh;
     const uint8_t* mk = a.mask + b * a.m_sb;
     const T* g = (const T*)a.go + b * a.g_sb + h * a.g_sh;
     const float* lse = a.lse + (int64_t)bh * L;
+    const float* dlt = a.delta + (int64_t)bh * L;
+
+    // A operand of dW^T = V dO^T: this wavefront's 32 V rows (k = head dim).
+    const int vkey = kb * 64 + kw + col;
+    const bool vkv = vkey < L;
+    const T* vrow = pw ? (const T*)a.vm + b * a.vm_sb + h * a.vm_sh + (int64_t)min(vkey, L - 1) * a.vm_st
+                       : (const T*)a.vs + b * a.vs_sb + h * a.vs_sh + (int64_t)min(vkey, L - 1) * a.vs_st;
+    constexpr int NS16 = ND * 2;
+    typename OpT<T>::type vop[F32 ? ND * 16 : NS16];
+    if constexpr (F32) {
+#pragma unroll
+        for (int c = 0; c < ND * 16; ++c) {
+            const int d = 2 * c + half;
+            vop[c] = (vkv && d < D) ? (float)vrow[d] : 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NS16; ++s) vop[s] = load8op<T>(vrow, s * 16 + half * 8, D, vkv);
+    }
 
     // Loader role: thread -> (query row tq of the chunk, 8-key group tg).
     const int tq = tid >> 3, tg = tid & 7;
@@ -488,38 +427,42 @@ __global__ __launch_bounds__(256) void combine_dv_kernel(CombineArgs a) {
 
     const int nch = D / 8;
     for (int q0 = 0; q0 < L; q0 += 32) {
+        const int qq = q0 + tq;
+        const int qc = min(qq, L - 1);
+        float p[8];
+        unsigned bits;
+        float dq;
         __syncthreads();
         {
-            const int qq = q0 + tq;
-            const int qc = min(qq, L - 1);
             float si[8], se[8];
             load_logits<T, 8, VEC>(il + (int64_t)qc * a.il_st, k8, L, si);
             load_logits<T, 8, VEC>(el + (int64_t)qc * a.el_st, k8, L, se);
-            const unsigned bits = load_mask<8, VEC>(mk + (int64_t)qc * a.m_sq, a.m_sk, k8, L);
+            bits = load_mask<8, VEC>(mk + (int64_t)qc * a.m_sq, a.m_sk, k8, L);
             const float l = lse[qc];
+            dq = dlt[qc];
             const bool ok = qq < L && l > -INFINITY;
             const float l2 = ok ? l * kLog2eC : 0.f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const bool x = (bits >> j) & 1;
-                const float p = ok ? fast_exp2((x ? se[j] : si[j]) * kLog2eC - l2) : 0.f;
+                p[j] = ok ? fast_exp2((x ? se[j] : si[j]) * kLog2eC - l2) : 0.f;
                 if constexpr (F32) {
                     float* P = (float*)lp;
-                    P[tq * PF_RS + tg * 8 + j] = x ? 0.f : p;
-                    P[32 * PF_RS + tq * PF_RS + tg * 8 + j] = x ? p : 0.f;
+                    P[tq * PF_RS + tg * 8 + j] = x ? 0.f : p[j];
+                    P[32 * PF_RS + tq * PF_RS + tg * 8 + j] = x ? p[j] : 0.f;
                 } else {
-                    lp[(tg * 8 + j) * PT_RS + tq] = (T)(x ? 0.f : p);
-                    lp[64 * PT_RS + (tg * 8 + j) * PT_RS + tq] = (T)(x ? p : 0.f);
+                    lp[(tg * 8 + j) * PT_RS + tq] = (T)(x ? 0.f : p[j]);
+                    lp[64 * PT_RS + (tg * 8 + j) * PT_RS + tq] = (T)(x ? p[j] : 0.f);
                 }
             }
         }
         // dO rows q0 .. q0+31 (rows >= L and dims >= D are zero).
         for (int c = tid; c < 32 * (DP / 8); c += 256) {
             const int r = c / (DP / 8), dc = c - r * (DP / 8);
-            const int qq = q0 + r;
+            const int qr = q0 + r;
             float x[8];
-            if (qq < L && dc < nch) {
-                const T* src = g + (int64_t)qq * a.g_st + dc * 8;
+            if (qr < L && dc < nch) {
+                const T* src = g + (int64_t)qr * a.g_st + dc * 8;
 #pragma unroll
                 for (int j = 0; j < 8; j += 4) load4f<T>(src, j, x + j);
             } else {
@@ -533,12 +476,20 @@ __global__ __launch_bounds__(256) void combine_dv_kernel(CombineArgs a) {
             } else {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) lg[(dc * 8 + j) * GT_RS + r] = (T)x[j];
+                typename CT<T>::v8 xv;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xv[j] = (T)x[j];
+                *reinterpret_cast<typename CT<T>::v8*>(lgr + r * GR_RS + dc * 8) = xv;
             }
         }
         __syncthreads();
+        f32x16 dw;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dw[i] = 0.f;
         if constexpr (F32) {
             const float* P = (const float*)lp + pw * 32 * PF_RS + kw + col;
             const float* G = (const float*)lg + col;
+            const float* Gq = (const float*)lg + col * GF_RS;
 #pragma unroll 4
             for (int c = 0; c < 16; ++c) {
                 const int qr = 2 * c + half;
@@ -548,6 +499,9 @@ __global__ __launch_bounds__(256) void combine_dv_kernel(CombineArgs a) {
                     acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(G[qr * GF_RS + n * 32], bp, acc[n],
                                                                   0, 0, 0);
             }
+#pragma unroll
+            for (int c = 0; c < ND * 16; ++c)
+                dw = __builtin_amdgcn_mfma_f32_32x32x2f32(vop[c], Gq[2 * c + half], dw, 0, 0, 0);
         } else {
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
@@ -559,6 +513,43 @@ __global__ __launch_bounds__(256) void combine_dv_kernel(CombineArgs a) {
                         lg + (n * 32 + col) * GT_RS + s * 16 + half * 8);
                     acc[n] = Elt<T>::mma(ag, bp, acc[n]);
                 }
+            }
+#pragma unroll
+            for (int s = 0; s < NS16; ++s) {
+                const typename Elt<T>::v8 bg = *reinterpret_cast<const typename Elt<T>::v8*>(
+                    lgr + col * GR_RS + s * 16 + half * 8);
+                dw = Elt<T>::mma(vop[s], bg, dw);
+            }
+        }
+        // dW^T accumulator slot 4*gi + r: key kw + 8*gi + 4*half + r, query col.
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi)
+            *reinterpret_cast<f32x4*>(lw + pw * 32 * W_RS + col * W_RS + kw + gi * 8 + half * 4) =
+                f32x4{dw[gi * 4], dw[gi * 4 + 1], dw[gi * 4 + 2], dw[gi * 4 + 3]};
+        __syncthreads();
+        if (qq < L) {
+            const float* ws = lw + tq * W_RS + tg * 8;
+            const float* wm = ws + 32 * W_RS;
+            float di[8], de[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const bool x = (bits >> j) & 1;
+                const float ds = p[j] * ((x ? wm[j] : ws[j]) - dq);
+                di[j] = x ? 0.f : ds;
+                de[j] = x ? ds : 0.f;
+            }
+            T* ri = dil + (int64_t)qq * a.dil_st;
+            T* re = del + (int64_t)qq * a.del_st;
+            if (VEC && k8 + 8 <= L) {
+                store8<T>(ri, k8, di);
+                store8<T>(re, k8, de);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (k8 + j < L) {
+                        ri[k8 + j] = (T)di[j];
+                        re[k8 + j] = (T)de[j];
+                    }
             }
         }
     }
@@ -590,8 +581,7 @@ hipError_t launch_combine_t(const CombineArgs& a, int mode, hipStream_t st) {
         hipLaunchKernelGGL((combine_fwd_kernel<T, ND, VEC, false>), dim3(bh * nqb), dim3(256), 0, st, a);
     } else {
         hipLaunchKernelGGL((combine_fwd_kernel<T, ND, VEC, true>), dim3(bh * nqb), dim3(256), 0, st, a);
-        hipLaunchKernelGGL((combine_dlogits_kernel<T, ND, VEC>), dim3(bh * nqb), dim3(256), 0, st, a);
-        hipLaunchKernelGGL((combine_dv_kernel<T, ND, VEC>), dim3(bh * nkb), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((combine_bwd_kernel<T, ND, VEC>), dim3(bh * nkb), dim3(256), 0, st, a);
     }
     return hipGetLastError();
 }
