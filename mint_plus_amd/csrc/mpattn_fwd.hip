@@ -183,35 +183,48 @@ template <int D> struct FwdShape : TileShape<D> {
     static constexpr int NKK = DP / 16;                              // QK MFMAs / subtile
     static constexpr int NDB = DP <= 32 ? 1 : 2;                     // 32-row blocks of O^T
     static constexpr int STAGE = 4 * TileShape<D>::TILE;             // K_s, K_m, V_s, V_m
-    static constexpr int W = D == 64 ? 4 : 8;                        // wavefronts per workgroup
 };
 
-#ifndef MPATTN_FWD_WAVES
-#define MPATTN_FWD_WAVES 4  // register budget: wavefronts per SIMD
+#ifndef MPATTN_FWD_QB
+// 32-query blocks per wavefront for D <= 32. Two blocks halve the per-stage
+// bookkeeping, barriers and LDS operand reads per flop and let the logits of
+// one block be computed on the matrix cores while the other block's softmax
+// runs on the VALU; the register budget is then 2 wavefronts per SIMD.
+#define MPATTN_FWD_QB 1
 #endif
 #ifndef MPATTN_FWD_NBUF
 #define MPATTN_FWD_NBUF 2  // LDS stages in the copy ring (copies run NBUF-1 stages ahead)
 #endif
-#ifndef MPATTN_FWD_SPLIT
-// Key halves per 32-query block (D <= 32). 2 fills the machine in whole rounds
-// at the 150M shape but doubles the per-task prologue and the L2->LDS copies;
-// measured on MI355X it is slower (145 us vs 121 us), so the default is 1.
-#define MPATTN_FWD_SPLIT 1
-#endif
+
+// Launch shape per head dim: W wavefronts per workgroup, QB query blocks per
+// wavefront, WPE wavefronts per SIMD (the register budget).
+template <int D> struct FwdCfg {
+    static constexpr int QB = D == 64 ? 1 : MPATTN_FWD_QB;
+    static constexpr int W = QB == 1 ? (D == 64 ? 4 : 8) : 4;
+    static constexpr int WPE = QB == 1 ? 4 : 2;
+};
 
 // Row sums above this bound (or not finite) send a stage through the fix-up
 // path, which moves the row's reference max. 2^64 keeps every partial sum and
 // accumulator far from fp32 overflow.
 constexpr float kSumHi = 18446744073709551616.0f;
 
-// SPLIT = 2: two wavefronts per 32-query block, each over half of the keys,
-// merged through LDS at the end; each half streams its keys through its own
-// LDS ring (both halves share the per-stage barrier).
+template <int N> using IC = std::integral_constant<int, N>;
+
+// Calls f(IC<0>{}), ..., f(IC<N-1>{}): per-block state is indexed by compile-
+// time constants only, so it stays in registers.
+template <int N, typename F> __device__ __forceinline__ void for_blocks(F&& f) {
+    if constexpr (N > 0) {
+        for_blocks<N - 1>(f);
+        f(IC<N - 1>{});
+    }
+}
+
 // SQRT: sqrt-softmax, O = sum_j sqrt(P_ij) V_j. The kernel then works with
 // e = exp2(s2 / 2) (the 1/2 is folded into the logit factor), accumulates
 // sum e V and sum e^2, and divides by sqrt(sum e^2) at the end.
-template <typename T, int D, int W, int SPLIT, int NBUF, bool ROPE, bool DENSE, bool SQRT>
-__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(MPATTN_FWD_WAVES)))
+template <typename T, int D, int W, int QB, int WPE, int NBUF, bool ROPE, bool DENSE, bool SQRT>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void fwd_kernel(const FwdArgs args) {
     using S = FwdShape<D>;
     using E = Elt<T>;
@@ -219,30 +232,34 @@ void fwd_kernel(const FwdArgs args) {
     typedef typename E::v2 v2;
     typedef short s4 __attribute__((ext_vector_type(4)));
     static_assert(NBUF >= 2 && NBUF <= 4, "LDS stages in flight");
-    static_assert(SPLIT == 1 || SPLIT == 2, "key split");
-    constexpr int WQ = W / SPLIT;               // 32-query blocks per workgroup
-    constexpr int TOT = 4 * S::NI;              // DMA wave-instructions per full stage
-    constexpr int NJ = (TOT + WQ - 1) / WQ;     // per wavefront (the last may be idle)
+    static_assert(QB == 1 || QB == 2, "query blocks per wavefront");
+    constexpr int QW = 32 * QB;              // queries per wavefront
+    constexpr int TOT = 4 * S::NI;           // DMA wave-instructions per full stage
+    constexpr int NJ = (TOT + W - 1) / W;    // per wavefront (the last may be idle)
     // With fused RoPE the logit factor scale*log2(e) is folded into Q.
     constexpr bool FOLDED = ROPE;
     const mpattn_fwd_params& p = args.p;
 
-    __shared__ __attribute__((aligned(1024))) char smem[SPLIT * NBUF * S::STAGE];
+    __shared__ __attribute__((aligned(1024))) char smem[NBUF * S::STAGE];
     __shared__ __attribute__((aligned(16))) int scid[W][NBUF][kBN];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
     const int L = p.L, H = p.H, Lp = args.Lp;
-    const int half = SPLIT == 1 ? 0 : wave / WQ;  // key half of this wavefront
-    const int qw = wave - half * WQ;              // its query block in the workgroup
-    const int nqb = (L + 32 * WQ - 1) / (32 * WQ);
+    const int nqb = (L + QW * W - 1) / (QW * W);
     const int g = xcd_remap(blockIdx.x, gridDim.x);
     const int qb = g % nqb, bh = g / nqb;
     const int b = bh / H, h = bh % H;
-    const int qw0 = qb * 32 * WQ;  // first query of the workgroup
-    const int q = qw0 + qw * 32 + ql;
-    const bool qvalid = q < L;
+    const int qw0 = qb * QW * W;    // first query of the workgroup
+    const int qv0 = qw0 + wave * QW;  // first query of this wavefront
+    int qrow[QB];
+    bool qvalid[QB];
+#pragma unroll
+    for (int u = 0; u < QB; ++u) {
+        qrow[u] = qv0 + 32 * u + ql;
+        qvalid[u] = qrow[u] < L;
+    }
 
     auto base = [&](const mpattn_tensor& t) {
         return (const T*)t.ptr + b * t.stride_b + h * t.stride_h;
@@ -269,7 +286,7 @@ void fwd_kernel(const FwdArgs args) {
     int dten[NJ];         // tile index, 4 for an idle copy (uniform)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        const int ins0 = qw + j * WQ;
+        const int ins0 = wave + j * W;
         const int ins = ins0 < TOT ? ins0 : TOT - 1;
         const int ten = ins / S::NI, part = ins % S::NI;
         const int slot = part * 64 + lane;
@@ -285,7 +302,7 @@ void fwd_kernel(const FwdArgs args) {
         dloff[j] = r * dstr[j] + cb;
         dten[j] = ins0 < TOT ? ten : 4;
     }
-    const unsigned smem_base = lds_addr(smem) + half * NBUF * S::STAGE;  // this half's ring
+    const unsigned smem_base = lds_addr(smem);
     const unsigned scid_base = lds_addr(&scid[wave][0][0]);
 
     // ---- copy stage s into buffer bf: only the pathways the workgroup needs ----
@@ -314,67 +331,95 @@ void fwd_kernel(const FwdArgs args) {
         return n;
     };
 
+    // Stage 0 is copied first, with every tile, so its copy overlaps the
+    // prologue loads below instead of waiting for the chain summaries that
+    // decide which tiles later stages need.
+    const int nst = (L + kBN - 1) / kBN;
+    int pend[NBUF];
+#pragma unroll
+    for (int t = 0; t < NBUF; ++t) pend[t] = 0;
+    pend[0] = issue(0, 0, 15);
+
     // ---- Q fragments (B operand of S^T = K Q^T): dims kk*16 + 8*hh + [0,8) ----
-    v8 qf[2][S::NKK];
+    v8 qf[QB][2][S::NKK];
 #pragma unroll
-    for (int pw = 0; pw < 2; ++pw) {
+    for (int u = 0; u < QB; ++u)
 #pragma unroll
-        for (int kk = 0; kk < S::NKK; ++kk) {
-            float x[8];
-            if (qvalid) {
-                const T* row = pw == 0 ? qs_p + (int64_t)q * p.q_self.stride_t
-                                       : qm_p + (int64_t)q * p.q_multi.stride_t;
-                load8_rot<T, D>(row, p.rope_cos, p.rope_sin, q, kk * 16 + hh * 8, args.qmul,
-                                ROPE && pw == 0, x);
-            } else {
+        for (int pw = 0; pw < 2; ++pw)
 #pragma unroll
-                for (int t = 0; t < 8; ++t) x[t] = 0.f;
+            for (int kk = 0; kk < S::NKK; ++kk) {
+                float x[8];
+                if (qvalid[u]) {
+                    const T* row = pw == 0 ? qs_p + (int64_t)qrow[u] * p.q_self.stride_t
+                                           : qm_p + (int64_t)qrow[u] * p.q_multi.stride_t;
+                    load8_rot<T, D>(row, p.rope_cos, p.rope_sin, qrow[u], kk * 16 + hh * 8, args.qmul,
+                                    ROPE && pw == 0, x);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) x[t] = 0.f;
+                }
+                qf[u][pw][kk] = pack8<T>(x);
             }
-            qf[pw][kk] = pack8<T>(x);
-        }
-    }
-    // Query chain ranges of this wavefront and of the whole workgroup.
-    // (from the per-32-query summaries of the prep kernel: uniform loads)
-    int cq = 0, cq_min = 0, cq_max = 0, wq_min = INT32_MAX, wq_max = INT32_MIN;
+    // Query chain ranges of each block and of the whole workgroup
+    // (from the per-32-query summaries of the prep kernel: uniform loads).
+    int cq[QB], cq_min[QB], cq_max[QB];
+    int wq_min = INT32_MAX, wq_max = INT32_MIN;
+#pragma unroll
+    for (int u = 0; u < QB; ++u) cq[u] = cq_min[u] = cq_max[u] = 0;
     if constexpr (!DENSE) {
-        cq = qvalid ? p.chain_id[(int64_t)b * L + q] : 0;
+#pragma unroll
+        for (int u = 0; u < QB; ++u) cq[u] = qvalid[u] ? p.chain_id[(int64_t)b * L + qrow[u]] : 0;
         const int4* qsum_b = reinterpret_cast<const int4*>(args.qsum) + (int64_t)b * (Lp / 32) + qw0 / 32;
 #pragma unroll
-        for (int w = 0; w < WQ; ++w) {
+        for (int w = 0; w < W * QB; ++w) {
             const int4 qs = qsum_b[w < Lp / 32 - qw0 / 32 ? w : 0];
             if (qw0 + 32 * w < L) {
                 wq_min = min(wq_min, qs.x);
                 wq_max = max(wq_max, qs.y);
             }
-            if (w == qw) {
-                cq_min = qs.x;
-                cq_max = qs.y;
-            }
+#pragma unroll
+            for (int u = 0; u < QB; ++u)
+                if (w == wave * QB + u) {
+                    cq_min[u] = qs.x;
+                    cq_max[u] = qs.y;
+                }
         }
         wq_min = __builtin_amdgcn_readfirstlane(wq_min);
         wq_max = __builtin_amdgcn_readfirstlane(wq_max);
-        cq_min = __builtin_amdgcn_readfirstlane(cq_min);
-        cq_max = __builtin_amdgcn_readfirstlane(cq_max);
+#pragma unroll
+        for (int u = 0; u < QB; ++u) {
+            cq_min[u] = __builtin_amdgcn_readfirstlane(cq_min[u]);
+            cq_max[u] = __builtin_amdgcn_readfirstlane(cq_max[u]);
+        }
     }
-    const uint8_t* mrow = nullptr;
-    if constexpr (DENSE) {
-        mrow = p.chain_mask + (int64_t)b * p.mask_stride_b + (int64_t)(qvalid ? q : 0) * p.mask_stride_q;
+    const uint8_t* mrow[QB];
+#pragma unroll
+    for (int u = 0; u < QB; ++u) {
+        mrow[u] = nullptr;
+        if constexpr (DENSE)
+            mrow[u] = p.chain_mask + (int64_t)b * p.mask_stride_b +
+                      (int64_t)(qvalid[u] ? qrow[u] : 0) * p.mask_stride_q;
     }
 
-    // ---- softmax state ----
+    // ---- softmax state, per query block ----
     // Probabilities are exp2(s2 - m_ref) with s2 = c * s the base-2 logit.
     // m_ref starts at 0 and stays there unless a stage's row sum leaves
     // (0, 2^64]: then the fix-up path sets it from that stage's max and the
-    // wavefront switches to the shifted form (one FMA per logit).
+    // block switches to the shifted form (one FMA per logit).
     const float c = args.c;  // 1 when FOLDED
-    float m_ref = 0.f;
-    bool shifted = false;    // wavefront-uniform: some m_ref != 0
-    float l_run = 0.f;
-    f32x16 o[S::NDB];
+    float m_ref[QB], l_run[QB];
+    bool shifted[QB];         // wavefront-uniform: some m_ref != 0
+    f32x16 o[QB][S::NDB];
 #pragma unroll
-    for (int db = 0; db < S::NDB; ++db)
+    for (int u = 0; u < QB; ++u) {
+        m_ref[u] = 0.f;
+        l_run[u] = 0.f;
+        shifted[u] = false;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+        for (int db = 0; db < S::NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[u][db][i] = 0.f;
+    }
 
     const int krow = swapped_row(ql);
     v8 zero8;
@@ -405,14 +450,14 @@ void fwd_kernel(const FwdArgs args) {
         }
     }
 
-    // Base-2 probability of raw logit x.
-    auto prob = [&](float x, bool sh) -> float {
-        if (sh) return fast_exp2(fmaf(x, c, -m_ref));
+    // Base-2 probability of raw logit x against reference mr.
+    auto prob = [&](float x, bool sh, float mr) -> float {
+        if (sh) return fast_exp2(fmaf(x, c, -mr));
         return fast_exp2(FOLDED ? x : x * c);
     };
     // Probabilities of NS subtiles (slot 8*cc + t -> pb[st][cc][t]) and their
     // row sum over this lane's keys.
-    auto probs = [&](auto ns_c, const f32x16* sv, v8 (*pb)[2], bool sh) -> float {
+    auto probs = [&](auto ns_c, const f32x16* sv, v8 (*pb)[2], bool sh, float mr) -> float {
         constexpr int NS = decltype(ns_c)::value;
         typedef float f32x2 __attribute__((ext_vector_type(2)));
         // Pairs are rounded once (v_cvt_pk) and feed both the PV operand and
@@ -424,9 +469,10 @@ void fwd_kernel(const FwdArgs args) {
             for (int cc = 0; cc < 2; ++cc) {
                 v2 pr[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const f32x2 f = {prob(sv[st][8 * cc + 2 * u], sh), prob(sv[st][8 * cc + 2 * u + 1], sh)};
-                    pr[u] = __builtin_convertvector(f, v2);
+                for (int uu = 0; uu < 4; ++uu) {
+                    const f32x2 f = {prob(sv[st][8 * cc + 2 * uu], sh, mr),
+                                     prob(sv[st][8 * cc + 2 * uu + 1], sh, mr)};
+                    pr[uu] = __builtin_convertvector(f, v2);
                 }
                 pb[st][cc] = __builtin_shufflevector(__builtin_shufflevector(pr[0], pr[1], 0, 1, 2, 3),
                                                      __builtin_shufflevector(pr[2], pr[3], 0, 1, 2, 3), 0, 1, 2,
@@ -446,37 +492,35 @@ void fwd_kernel(const FwdArgs args) {
         return ls0 + ls1;
     };
     // Rare path: a lane's stage sum overflowed, or its row has accumulated
-    // nothing yet. The stage's logits are recomputed from LDS (`logits`
+    // nothing yet. The subtile's logits are recomputed from LDS (`logits`
     // fills sv) and its probabilities redone relative to a reference max
     // taken from them (raised only, once something has been accumulated).
-    auto fixup = [&](auto ns_c, auto logits, v8 (*pb)[2]) -> float {
-        constexpr int NS = decltype(ns_c)::value;
-        f32x16 sv[NS];
+    auto fixup = [&](auto u_c, auto logits, v8 (*pb)[2]) -> float {
+        constexpr int u = decltype(u_c)::value;
+        f32x16 sv[1];
         logits(sv);
         float mx = -INFINITY;
 #pragma unroll
-        for (int st = 0; st < NS; ++st)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sv[st][i]);
-        const float mq = fmaxf(mx, __shfl_xor(mx, 32));  // query max of the stage, raw units
-        const float lq = l_run + __shfl_xor(l_run, 32);
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sv[0][i]);
+        const float mq = fmaxf(mx, __shfl_xor(mx, 32));  // query max of the subtile, raw units
+        const float lq = l_run[u] + __shfl_xor(l_run[u], 32);
         const float ms = mq * c;
         float m_new;
-        if (lq > 0.f) m_new = fmaxf(m_ref, ms);
-        else m_new = ms > -INFINITY ? ms : m_ref;
-        const float alpha = lq > 0.f ? fast_exp2(m_ref - m_new) : 1.0f;
-        l_run *= SQRT ? alpha * alpha : alpha;
+        if (lq > 0.f) m_new = fmaxf(m_ref[u], ms);
+        else m_new = ms > -INFINITY ? ms : m_ref[u];
+        const float alpha = lq > 0.f ? fast_exp2(m_ref[u] - m_new) : 1.0f;
+        l_run[u] *= SQRT ? alpha * alpha : alpha;
 #pragma unroll
         for (int db = 0; db < S::NDB; ++db)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-        m_ref = m_new;
-        shifted = __builtin_amdgcn_ballot_w64(m_ref != 0.f) != 0;
-        return probs(ns_c, sv, pb, true);
+            for (int i = 0; i < 16; ++i) o[u][db][i] *= alpha;
+        m_ref[u] = m_new;
+        shifted[u] = __builtin_amdgcn_ballot_w64(m_new != 0.f) != 0;
+        return probs(IC<1>{}, sv, pb, true, m_new);
     };
-    // Stage check: true if any lane needs the fix-up.
-    auto needs_fix = [&](float ls) {
-        const bool bad = !(ls <= kSumHi) || (l_run + ls == 0.f);
+    // Check: true if any lane of block u needs the fix-up.
+    auto needs_fix = [&](float ls, float lr) {
+        const bool bad = !(ls <= kSumHi) || (lr + ls == 0.f);
         return __builtin_amdgcn_ballot_w64(bad) != 0;
     };
 
@@ -504,18 +548,21 @@ void fwd_kernel(const FwdArgs args) {
         for (int kk = 0; kk < S::NKK; ++kk) sv = E::mma(ka[kk], qa[kk], sv);
         return sv;
     };
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
 
-    // Q operand of the fast path's pathway (changes rarely: at chain edges).
+    // Q operands of the fast path's pathway (changes rarely: at chain edges).
     int cur_pw = 0;
-    v8 qcur[S::NKK];
+    v8 qcur[QB][S::NKK];
 #pragma unroll
-    for (int kk = 0; kk < S::NKK; ++kk) qcur[kk] = qf[0][kk];
+    for (int u = 0; u < QB; ++u)
+#pragma unroll
+        for (int kk = 0; kk < S::NKK; ++kk) qcur[u][kk] = qf[u][0][kk];
 
-    // Fast path: both subtiles of the stage on pathway pw, unshifted softmax.
-    // Returns false (nothing accumulated) if the stage needs the fix-up.
-    auto fast_stage = [&](const char* stage, int pw) -> bool {
+    // Fast path: every block and both subtiles of the stage on pathway pw,
+    // unshifted softmax. All blocks' logits are issued first so the matrix
+    // cores work on block u+1 while the VALU does block u's softmax. Returns
+    // the mask of blocks accumulated; a block that needs the fix-up is left
+    // to the slow path.
+    auto fast_stage = [&](const char* stage, int pw) -> int {
         const char* kt = stage + pw * S::TILE;
         const char* vt = stage + (2 + pw) * S::TILE;
         // All LDS operands are read up front: the V reads overlap the softmax.
@@ -532,27 +579,33 @@ void fwd_kernel(const FwdArgs args) {
                 for (int db = 0; db < S::NDB; ++db) va[st][cc][db] = vop_t(vt, st, cc, db);
         // keep every LDS read of the stage ahead of the softmax
         __builtin_amdgcn_sched_barrier(0);
-        v8 pb[2][2];
-        float ls;
-        {
-            f32x16 sv[2];
+        f32x16 sv[QB][2];
 #pragma unroll
-            for (int st = 0; st < 2; ++st) sv[st] = qkq(ka[st], qcur);
-            ls = probs(I2{}, sv, pb, false);
-        }
-        if (needs_fix(ls)) return false;
-        l_run += ls;
+        for (int u = 0; u < QB; ++u)
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+            for (int st = 0; st < 2; ++st) sv[u][st] = qkq(ka[st], qcur[u]);
+        int done = 0;
+        for_blocks<QB>([&](auto u_c) {
+            constexpr int u = decltype(u_c)::value;
+            v8 pb[2][2];
+            const float ls = probs(IC<2>{}, sv[u], pb, false, 0.f);
+            if (needs_fix(ls, l_run[u])) return;
+            l_run[u] += ls;
+            done |= 1 << u;
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc)
+            for (int st = 0; st < 2; ++st)
 #pragma unroll
-                for (int db = 0; db < S::NDB; ++db) o[db] = E::mma(va[st][cc][db], pb[st][cc], o[db]);
-        return true;
+                for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+                    for (int db = 0; db < S::NDB; ++db) o[u][db] = E::mma(va[st][cc][db], pb[st][cc], o[u][db]);
+        });
+        return done;
     };
 
-    // Both pathways on one subtile, selected per element; handles padded keys.
-    auto general = [&](const char* stage, const int* cid, int st, int k0) {
+    // Both pathways on one subtile of block u, selected per element; handles
+    // padded keys.
+    auto general = [&](auto u_c, const char* stage, const int* cid, int st, int k0) {
+        constexpr int u = decltype(u_c)::value;
         bool same[16];
         // Selected raw logits (-inf for padded keys) into sv[0]; keys of
         // slot i: st*32 + 16*(i/8) + 8*hh + i%8.
@@ -563,7 +616,7 @@ void fwd_kernel(const FwdArgs args) {
                 ks[kk] = kop_t(stage, st, kk);
                 km[kk] = kop_t(stage + S::TILE, st, kk);
             }
-            const f32x16 ss = qkq(ks, qf[0]), sm = qkq(km, qf[1]);
+            const f32x16 ss = qkq(ks, qf[u][0]), sm = qkq(km, qf[u][1]);
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 const int kl = st * 32 + 16 * cc + 8 * hh;
@@ -574,13 +627,13 @@ void fwd_kernel(const FwdArgs args) {
                     const int kg = k0 + kl;
                     for (int t = 0; t < 8; ++t)
                         if (kg + t < L)
-                            mbits |= (uint32_t)(mrow[(int64_t)(kg + t) * p.mask_stride_k] != 0) << t;
+                            mbits |= (uint32_t)(mrow[u][(int64_t)(kg + t) * p.mask_stride_k] != 0) << t;
                 }
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
                     const int ck = t < 4 ? c0[t & 3] : c1[t & 3];
                     const int i = 8 * cc + t;
-                    const bool sm_ = DENSE ? !((mbits >> t) & 1u) : (ck == cq);
+                    const bool sm_ = DENSE ? !((mbits >> t) & 1u) : (ck == cq[u]);
                     same[i] = sm_;
                     const float v = sm_ ? ss[i] : sm[i];
                     sv[0][i] = ck == kPadChain ? -INFINITY : v;
@@ -592,10 +645,10 @@ void fwd_kernel(const FwdArgs args) {
         {
             f32x16 sv[1];
             logits(sv);
-            ls = shifted ? probs(I1{}, sv, pb, true) : probs(I1{}, sv, pb, false);
+            ls = shifted[u] ? probs(IC<1>{}, sv, pb, true, m_ref[u]) : probs(IC<1>{}, sv, pb, false, 0.f);
         }
-        if (needs_fix(ls)) ls = fixup(I1{}, logits, pb);
-        l_run += ls;
+        if (needs_fix(ls, l_run[u])) ls = fixup(u_c, logits, pb);
+        l_run[u] += ls;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
             v8 ps, pm;
@@ -607,19 +660,20 @@ void fwd_kernel(const FwdArgs args) {
             }
 #pragma unroll
             for (int db = 0; db < S::NDB; ++db) {
-                o[db] = E::mma(vop_t(stage + 2 * S::TILE, st, cc, db), ps, o[db]);
-                o[db] = E::mma(vop_t(stage + 3 * S::TILE, st, cc, db), pm, o[db]);
+                o[u][db] = E::mma(vop_t(stage + 2 * S::TILE, st, cc, db), ps, o[u][db]);
+                o[u][db] = E::mma(vop_t(stage + 3 * S::TILE, st, cc, db), pm, o[u][db]);
             }
         }
     };
 
-    // One subtile on the slow path. code: 0 pure self, 1 pure multimer,
-    // 2 straddle (keys on one chain, queries on several: pathway per lane),
-    // 3 general, 4 skip.
-    auto slow_subtile = [&](const char* stage, const int* cid, int st, int code, int k0) {
+    // One subtile of block u on the slow path. code: 0 pure self, 1 pure
+    // multimer, 2 straddle (keys on one chain, queries on several: pathway per
+    // lane), 3 general, 4 skip.
+    auto slow_subtile = [&](auto u_c, const char* stage, const int* cid, int st, int code, int k0) {
+        constexpr int u = decltype(u_c)::value;
         if (code >= 4) return;
         if (code == 3) {
-            general(stage, cid, st, k0);
+            general(u_c, stage, cid, st, k0);
             return;
         }
         v8 pb[1][2];
@@ -629,7 +683,7 @@ void fwd_kernel(const FwdArgs args) {
             const char* kt = stage + pw * S::TILE;
             v8 qa[S::NKK];
 #pragma unroll
-            for (int kk = 0; kk < S::NKK; ++kk) qa[kk] = pw ? qf[1][kk] : qf[0][kk];
+            for (int kk = 0; kk < S::NKK; ++kk) qa[kk] = pw ? qf[u][1][kk] : qf[u][0][kk];
             auto logits = [&](f32x16* sv) {
                 v8 kr[S::NKK];
 #pragma unroll
@@ -639,19 +693,19 @@ void fwd_kernel(const FwdArgs args) {
             {
                 f32x16 sv[1];
                 logits(sv);
-                ls = shifted ? probs(I1{}, sv, pb, true) : probs(I1{}, sv, pb, false);
+                ls = shifted[u] ? probs(IC<1>{}, sv, pb, true, m_ref[u]) : probs(IC<1>{}, sv, pb, false, 0.f);
             }
-            if (needs_fix(ls)) ls = fixup(I1{}, logits, pb);
-            l_run += ls;
+            if (needs_fix(ls, l_run[u])) ls = fixup(u_c, logits, pb);
+            l_run[u] += ls;
             const char* vt = stage + (2 + pw) * S::TILE;
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-                for (int db = 0; db < S::NDB; ++db) o[db] = E::mma(vop_t(vt, st, cc, db), pb[0][cc], o[db]);
+                for (int db = 0; db < S::NDB; ++db) o[u][db] = E::mma(vop_t(vt, st, cc, db), pb[0][cc], o[u][db]);
             return;
         }
         // straddle: lane is on the self pathway iff its chain is the keys' chain
-        const bool self_lane = cq == cid[st * 32];
+        const bool self_lane = cq[u] == cid[st * 32];
         auto logits = [&](f32x16* sv) {
             v8 ks[S::NKK], km[S::NKK];
 #pragma unroll
@@ -659,93 +713,93 @@ void fwd_kernel(const FwdArgs args) {
                 ks[kk] = kop_t(stage, st, kk);
                 km[kk] = kop_t(stage + S::TILE, st, kk);
             }
-            const f32x16 ss = qkq(ks, qf[0]), sm = qkq(km, qf[1]);
+            const f32x16 ss = qkq(ks, qf[u][0]), sm = qkq(km, qf[u][1]);
 #pragma unroll
             for (int i = 0; i < 16; ++i) sv[0][i] = self_lane ? ss[i] : sm[i];
         };
         {
             f32x16 sv[1];
             logits(sv);
-            ls = shifted ? probs(I1{}, sv, pb, true) : probs(I1{}, sv, pb, false);
+            ls = shifted[u] ? probs(IC<1>{}, sv, pb, true, m_ref[u]) : probs(IC<1>{}, sv, pb, false, 0.f);
         }
-        if (needs_fix(ls)) ls = fixup(I1{}, logits, pb);
-        l_run += ls;
+        if (needs_fix(ls, l_run[u])) ls = fixup(u_c, logits, pb);
+        l_run[u] += ls;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
             const v8 ps = self_lane ? pb[0][cc] : zero8;
             const v8 pm = self_lane ? zero8 : pb[0][cc];
 #pragma unroll
             for (int db = 0; db < S::NDB; ++db) {
-                o[db] = E::mma(vop_t(stage + 2 * S::TILE, st, cc, db), ps, o[db]);
-                o[db] = E::mma(vop_t(stage + 3 * S::TILE, st, cc, db), pm, o[db]);
+                o[u][db] = E::mma(vop_t(stage + 2 * S::TILE, st, cc, db), ps, o[u][db]);
+                o[u][db] = E::mma(vop_t(stage + 3 * S::TILE, st, cc, db), pm, o[u][db]);
             }
         }
     };
 
-    auto subtile_mode = [&](int kmin, int kmax, int npad) -> int {
+    auto subtile_mode = [&](int kmin, int kmax, int npad, int qmin, int qmax) -> int {
         if (npad == 32) return 4;
         if (DENSE) return 3;
         if (npad == 0) {
-            if (kmax < cq_min || kmin > cq_max) return 1;
-            if (kmin == kmax) return cq_min == cq_max ? 0 : 2;
+            if (kmax < qmin || kmin > qmax) return 1;
+            if (kmin == kmax) return qmin == qmax ? 0 : 2;
         }
         return 3;
     };
 
-    // Subtile codes of this wavefront for the 64 subtiles from kb0, as three
-    // bit masks (mb0..mb2 = code bits), and which pathways the workgroup
+    // Subtile codes of each block for the 64 subtiles from kb0, as three bit
+    // masks per block (mb0..mb2 = code bits), and which pathways the workgroup
     // needs there (nS / nM) so stages copy only those tiles. Each reload is a
     // vector load whose wait also drains the copies in flight: windows move
     // once per 32 stages.
-    uint64_t mb0 = 0, mb1 = 0, mb2 = 0, nS = 0, nM = 0;
-    auto load_codes = [&](int kb0) {
+    uint64_t mb0[QB], mb1[QB], mb2[QB], nS = 0, nM = 0;
+    auto ksum_at = [&](int kb0) -> int4 {
         const int kb = kb0 + lane;
-        int code = 4;
-        if (kb < Lp / 32) {
-            const int4 sm = ksum_b[kb];
-            code = subtile_mode(sm.x, sm.y, sm.z);
-        }
-        mb0 = __builtin_amdgcn_ballot_w64(code & 1);
-        mb1 = __builtin_amdgcn_ballot_w64((code >> 1) & 1);
-        mb2 = __builtin_amdgcn_ballot_w64((code >> 2) & 1);
+        int4 sm = {0, 0, 32, 0};
+        if (kb < Lp / 32) sm = ksum_b[kb];
+        return sm;
     };
-    auto load_needs = [&](int kb0) {
-        const int kb = kb0 + lane;
+    auto set_codes = [&](const int4 sm) {
+#pragma unroll
+        for (int u = 0; u < QB; ++u) {
+            const int code = subtile_mode(sm.x, sm.y, sm.z, cq_min[u], cq_max[u]);
+            mb0[u] = __builtin_amdgcn_ballot_w64(code & 1);
+            mb1[u] = __builtin_amdgcn_ballot_w64((code >> 1) & 1);
+            mb2[u] = __builtin_amdgcn_ballot_w64((code >> 2) & 1);
+        }
+    };
+    auto set_needs = [&](const int4 sm) {
         bool ns = false, nm = false;
-        if (kb < Lp / 32) {
-            const int4 sm = ksum_b[kb];
-            if (sm.z < 32) {
-                if (DENSE || sm.z > 0) {
-                    ns = nm = true;
-                } else {
-                    ns = !(sm.y < wq_min || sm.x > wq_max);
-                    nm = !(sm.x == sm.y && wq_min == wq_max && sm.x == wq_min);
-                }
+        if (sm.z < 32) {
+            if (DENSE || sm.z > 0) {
+                ns = nm = true;
+            } else {
+                ns = !(sm.y < wq_min || sm.x > wq_max);
+                nm = !(sm.x == sm.y && wq_min == wq_max && sm.x == wq_min);
             }
         }
         nS = __builtin_amdgcn_ballot_w64(ns);
         nM = __builtin_amdgcn_ballot_w64(nm);
     };
-    auto code_at = [&](int sub) -> int {
-        return (int)((mb0 >> sub) & 1) | (int)(((mb1 >> sub) & 1) << 1) | (int)(((mb2 >> sub) & 1) << 2);
+    auto load_codes = [&](int kb0) { set_codes(ksum_at(kb0)); };
+    auto load_needs = [&](int kb0) { set_needs(ksum_at(kb0)); };
+    auto code_at = [&](int u, int sub) -> int {
+        return (int)((mb0[u] >> sub) & 1) | (int)(((mb1[u] >> sub) & 1) << 1) |
+               (int)(((mb2[u] >> sub) & 1) << 2);
     };
 
     // ---- main loop over stages ----
-    // This wavefront's keys: stages [s_lo, s_lo + s_cnt); both halves run
-    // nloop iterations so the barriers pair up.
-    const int nst_all = (L + kBN - 1) / kBN;
-    const int n0 = SPLIT == 1 ? nst_all : (nst_all + 1) / 2;
-    const int s_lo = half ? n0 : 0;
-    const int s_cnt = half ? nst_all - n0 : n0;
-    const int nloop = n0;
-    int kbp = 2 * s_lo, kbi = 2 * s_lo;  // first subtile of the code / need windows
-    load_codes(kbp);                     // before any copy is in flight
-    load_needs(kbi);
-    // Every prologue load (Q, chain ids, summaries) has landed before the first
-    // copy is issued. The compiler sees this wait (the copies are inline asm it
+    int kbp = 0, kbi = 0;  // first subtile of the code / need windows
+    {
+        const int4 sm = ksum_at(0);
+        set_codes(sm);
+        set_needs(sm);
+    }
+    // Every prologue load (Q, chain ids, summaries) and the stage-0 copy have
+    // landed here. The compiler sees this wait (the copies are inline asm it
     // cannot see), so it adds no vmcnt(0) at later uses, which would also
     // drain the copies in flight.
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    pend[0] = 0;
     // Tiles stage t copies (bit i = tile i): K_self and V_self (bits 0, 2)
     // if any of its subtiles needs the self pathway, K_multi and V_multi
     // (1, 3) for the multimer pathway.
@@ -758,16 +812,13 @@ void fwd_kernel(const FwdArgs args) {
         const int m = (((nS >> nx) & 3) != 0 ? 5 : 0) | (((nM >> nx) & 3) != 0 ? 10 : 0);
         return __builtin_amdgcn_readfirstlane(m);
     };
-    // pend[k]: vector-memory instructions of local stage s + k still in flight.
-    int pend[NBUF];
+    // pend[k]: vector-memory instructions of stage s + k still in flight
+    // (stage 0 was issued before the prologue and has landed).
 #pragma unroll
-    for (int t = 0; t < NBUF; ++t) pend[t] = 0;
-#pragma unroll
-    for (int t = 0; t < NBUF - 1; ++t)
-        if (t < s_cnt) pend[t] = issue(s_lo + t, t, tiles_for(s_lo + t));
+    for (int t = 1; t < NBUF - 1; ++t)
+        if (t < nst) pend[t] = issue(t, t, tiles_for(t));
     int bf = 0;
-    char* const ring = smem + half * NBUF * S::STAGE;
-    for (int s = 0; s < nloop; ++s) {
+    for (int s = 0; s < nst; ++s) {
         int allow = 0;  // copies of later stages that may stay in flight
 #pragma unroll
         for (int k = 1; k < NBUF - 1; ++k) allow += pend[k];
@@ -776,105 +827,82 @@ void fwd_kernel(const FwdArgs args) {
 #pragma unroll
         for (int k = 0; k < NBUF - 1; ++k) pend[k] = pend[k + 1];
         pend[NBUF - 1] = 0;
-        if (s >= s_cnt) continue;  // the shorter half: barrier only
-        const int gs = s_lo + s;   // global stage index
-        if (2 * gs + 1 - kbp >= 64) {
-            kbp = 2 * gs;
+        if (2 * s + 1 - kbp >= 64) {
+            kbp = 2 * s;
             load_codes(kbp);
         }
-        const int sub = 2 * gs - kbp;
-        const int c0 = code_at(sub), c1 = code_at(sub + 1);
-        if (s + NBUF - 1 < s_cnt) {
+        const int sub = 2 * s - kbp;
+        int c0[QB], c1[QB];
+#pragma unroll
+        for (int u = 0; u < QB; ++u) {
+            c0[u] = code_at(u, sub);
+            c1[u] = code_at(u, sub + 1);
+        }
+        if (s + NBUF - 1 < nst) {
             const int bn = bf + NBUF - 1 >= NBUF ? bf - 1 : bf + NBUF - 1;
-            pend[NBUF - 2] = issue(gs + NBUF - 1, bn, tiles_for(gs + NBUF - 1));
+            pend[NBUF - 2] = issue(s + NBUF - 1, bn, tiles_for(s + NBUF - 1));
         }
 
-        const char* stage = ring + bf * S::STAGE;
-        bool done = false;
-        if (c0 == c1 && c0 <= 1 && !shifted) {
-            if (c0 != cur_pw) {  // rare: kept a branch (not selects on every stage)
-                asm volatile("" ::: "memory");
-                cur_pw = c0;
+        const char* stage = smem + bf * S::STAGE;
+        bool fast = c0[0] <= 1;
 #pragma unroll
-                for (int kk = 0; kk < S::NKK; ++kk) qcur[kk] = c0 ? qf[1][kk] : qf[0][kk];
+        for (int u = 0; u < QB; ++u) fast = fast && c0[u] == c0[0] && c1[u] == c0[0] && !shifted[u];
+        int done = 0;
+        if (fast) {
+            if (c0[0] != cur_pw) {  // rare: kept a branch (not selects on every stage)
+                asm volatile("" ::: "memory");
+                cur_pw = c0[0];
+#pragma unroll
+                for (int u = 0; u < QB; ++u)
+#pragma unroll
+                    for (int kk = 0; kk < S::NKK; ++kk) qcur[u][kk] = cur_pw ? qf[u][1][kk] : qf[u][0][kk];
             }
-            done = fast_stage(stage, c0);
+            done = fast_stage(stage, c0[0]);
         }
-        if (!done) {
+        if (done != (1 << QB) - 1) {
             const int* cid = &scid[wave][bf][0];
-            const int k0 = gs * kBN;
+            const int k0 = s * kBN;
+            for_blocks<QB>([&](auto u_c) {
+                constexpr int u = decltype(u_c)::value;
+                if ((done >> u) & 1) return;
 #pragma unroll 1
-            for (int st = 0; st < 2; ++st) slow_subtile(stage, cid, st, st ? c1 : c0, k0);
+                for (int st = 0; st < 2; ++st) slow_subtile(u_c, stage, cid, st, st ? c1[u] : c0[u], k0);
+            });
         }
         bf = bf + 1 == NBUF ? 0 : bf + 1;
     }
 
-    // ---- merge the two key halves (SPLIT = 2) ----
-    if constexpr (SPLIT == 2) {
-        // The rings are free once every wavefront passed its last stage.
-        stage_barrier();
-        constexpr int NV = 16 * S::NDB + 2;  // o, l_run, m_ref per lane
-        float* xs = reinterpret_cast<float*>(smem) + (size_t)qw * NV * 64;
-        if (half) {
+    // ---- epilogue: normalise, store O and LSE ----
+#pragma unroll
+    for (int u = 0; u < QB; ++u) {
+        const float l_tot = l_run[u] + __shfl_xor(l_run[u], 32);
+        const float inv = l_tot > 0.f ? (SQRT ? __frsqrt_rn(l_tot) : 1.0f / l_tot) : 0.f;
+        if (qvalid[u]) {
+            T* orow = (T*)p.out.ptr + b * p.out.stride_b + h * p.out.stride_h + (int64_t)qrow[u] * p.out.stride_t;
 #pragma unroll
             for (int db = 0; db < S::NDB; ++db)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) xs[(16 * db + i) * 64 + lane] = o[db][i];
-            xs[(16 * S::NDB) * 64 + lane] = l_run;
-            xs[(16 * S::NDB + 1) * 64 + lane] = m_ref;
-        }
-        stage_barrier();
-        if (half) return;
-        const float lb = xs[(16 * S::NDB) * 64 + lane];
-        const float mb = xs[(16 * S::NDB + 1) * 64 + lane];
-        // A half that accumulated nothing for this query (its sums over both
-        // lane halves are 0) neither sets nor rescales the merged reference.
-        const float laq = l_run + __shfl_xor(l_run, 32);
-        const float lbq = lb + __shfl_xor(lb, 32);
-        float m = m_ref;
-        if (lbq > 0.f) m = laq > 0.f ? fmaxf(m_ref, mb) : mb;
-        const float aa = (laq > 0.f && m_ref != m) ? fast_exp2(m_ref - m) : 1.0f;
-        const float ab = (lbq > 0.f && mb != m) ? fast_exp2(mb - m) : 1.0f;
+                for (int a = 0; a < 4; ++a) {
+                    const int d = db * 32 + 8 * a + 4 * hh;
+                    if (d < D) {
+                        typename E::v4 v;
 #pragma unroll
-        for (int db = 0; db < S::NDB; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[db][i] = o[db][i] * aa + xs[(16 * db + i) * 64 + lane] * ab;
-        l_run = SQRT ? l_run * aa * aa + lb * ab * ab : l_run * aa + lb * ab;
-        m_ref = m;
-    }
-
-    // ---- epilogue: normalise, store O and LSE ----
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
-    const float inv = l_tot > 0.f ? (SQRT ? __frsqrt_rn(l_tot) : 1.0f / l_tot) : 0.f;
-    if (qvalid) {
-        T* orow = (T*)p.out.ptr + b * p.out.stride_b + h * p.out.stride_h + (int64_t)q * p.out.stride_t;
-#pragma unroll
-        for (int db = 0; db < S::NDB; ++db)
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const int d = db * 32 + 8 * a + 4 * hh;
-                if (d < D) {
-                    typename E::v4 v;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) v[j] = (T)(o[db][4 * a + j] * inv);
-                    *reinterpret_cast<typename E::v4*>(orow + d) = v;
+                        for (int j = 0; j < 4; ++j) v[j] = (T)(o[u][db][4 * a + j] * inv);
+                        *reinterpret_cast<typename E::v4*>(orow + d) = v;
+                    }
                 }
+            if (p.lse && hh == 0) {
+                p.lse[((int64_t)b * H + h) * L + qrow[u]] =
+                    l_tot > 0.f ? ((SQRT ? 2.0f * m_ref[u] : m_ref[u]) + __log2f(l_tot)) * kLn2 : -INFINITY;
             }
-        if (p.lse && hh == 0) {
-            p.lse[((int64_t)b * H + h) * L + q] =
-                l_tot > 0.f ? ((SQRT ? 2.0f * m_ref : m_ref) + __log2f(l_tot)) * kLn2 : -INFINITY;
         }
     }
 }
 
 template <typename T, int D, bool ROPE, bool DENSE, bool SQRT>
 static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
-    constexpr int W = FwdShape<D>::W;
-    // Optional key split for D <= 32 (see MPATTN_FWD_SPLIT). Two LDS stages per
-    // ring keep two workgroups per CU with the split (D = 64 tiles are twice as
-    // large: two stages, no split).
-    constexpr int SPLIT = D == 64 ? 1 : MPATTN_FWD_SPLIT;
-    constexpr int NBUF = (D == 64 || SPLIT == 2) ? 2 : MPATTN_FWD_NBUF;
+    using C = FwdCfg<D>;
+    constexpr int NBUF = D == 64 ? 2 : MPATTN_FWD_NBUF;
     const mpattn_fwd_params& p = a.p;
     const int Lp = round_up(p.L, kBN);
     a.Lp = Lp;
@@ -895,11 +923,10 @@ static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
                        stream, p, keff, ksum, qsum, krot, Lp, nchain);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    constexpr int WQ = W / SPLIT;
-    const int nqb = (p.L + 32 * WQ - 1) / (32 * WQ);
+    const int nqb = (p.L + 32 * C::QB * C::W - 1) / (32 * C::QB * C::W);
     const int64_t grid = (int64_t)p.B * p.H * nqb;
-    hipLaunchKernelGGL((fwd_kernel<T, D, W, SPLIT, NBUF, ROPE, DENSE, SQRT>), dim3((unsigned)grid),
-                       dim3(W * 64), 0, stream, a);
+    hipLaunchKernelGGL((fwd_kernel<T, D, C::W, C::QB, C::WPE, NBUF, ROPE, DENSE, SQRT>), dim3((unsigned)grid),
+                       dim3(C::W * 64), 0, stream, a);
     return hipGetLastError();
 }
 
