@@ -208,6 +208,16 @@ __device__ __forceinline__ void dma4(const void* sbase, unsigned voff, unsigned 
                  :: "v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 
+// The same copies with a per-lane 64-bit global address (no scalar base).
+__device__ __forceinline__ void dma16v(const void* addr, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(addr), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4v(const void* addr, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :: "v"(addr), "s"(lds) : "memory");
+}
+
 // Wait until at most N vector-memory instructions of this wave are in flight.
 template <int N> __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");

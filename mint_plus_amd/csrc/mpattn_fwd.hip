@@ -280,8 +280,9 @@ void fwd_kernel(const FwdArgs args) {
     // 3 V_multi); lane -> (row r, logical chunk c), physical slot swizzled.
     const char* dsb[NJ];  // (b, h) base of the source tensor (uniform)
     unsigned dstr[NJ];    // row stride in bytes (uniform)
+    unsigned dinc[NJ];    // bytes between stages: 64 rows (uniform)
     unsigned dlds[NJ];    // LDS offset inside a stage (uniform)
-    unsigned dloff[NJ];   // per-lane byte offset of (r, c) relative to row 0
+    const char* dva[NJ];  // per-lane source address of (r, c) in stage 0
     int drow[NJ], dcol[NJ];
     int dten[NJ];         // tile index, 4 for an idle copy (uniform)
 #pragma unroll
@@ -296,37 +297,41 @@ void fwd_kernel(const FwdArgs args) {
         const int64_t ts = ten == 0 ? ks_t : ten == 1 ? km_t : ten == 2 ? vs_t : vm_t;
         dsb[j] = (const char*)tb;
         dstr[j] = (unsigned)(ts * (int64_t)sizeof(T));
+        dinc[j] = dstr[j] * kBN;
         dlds[j] = ten * S::TILE + part * 1024;
         drow[j] = r;
         dcol[j] = cb;
-        dloff[j] = r * dstr[j] + cb;
+        dva[j] = dsb[j] + (r * dstr[j] + cb);
         dten[j] = ins0 < TOT ? ten : 4;
     }
+    const char* const keff_lane = reinterpret_cast<const char*>(keff_b) + lane * 4;
     const unsigned smem_base = lds_addr(smem);
     const unsigned scid_base = lds_addr(&scid[wave][0][0]);
 
     // ---- copy stage s into buffer bf: only the pathways the workgroup needs ----
     // Returns the number of vector-memory instructions issued (uniform).
+    // Source rows are addressed per lane (64-bit): the row offset of a stage
+    // is s * 64 * stride, below 2^31 bytes (checked on the host).
     auto issue = [&](int s, int bf, int tiles) -> int {
         const int k0 = s * kBN;
         const unsigned lb = smem_base + bf * S::STAGE;
-        unsigned voff[NJ];
+        const char* va[NJ];
         if (k0 + kBN <= L) {
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) voff[j] = (unsigned)k0 * dstr[j] + dloff[j];
+            for (int j = 0; j < NJ; ++j) va[j] = dva[j] + (unsigned)s * dinc[j];
         } else {  // last stage: clamp rows past L to L-1 (their keys are masked)
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) voff[j] = (unsigned)min(k0 + drow[j], L - 1) * dstr[j] + dcol[j];
+            for (int j = 0; j < NJ; ++j) va[j] = dsb[j] + ((unsigned)min(k0 + drow[j], L - 1) * dstr[j] + dcol[j]);
         }
         const int m0v = m0_save();
         int n = 1;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
             if ((tiles >> dten[j]) & 1) {
-                dma16(dsb[j], voff[j], lb + dlds[j]);
+                dma16v(va[j], lb + dlds[j]);
                 ++n;
             }
-        dma4(keff_b, (unsigned)(k0 + lane) * 4u, scid_base + bf * kBN * 4);
+        dma4v(keff_lane + k0 * 4, scid_base + bf * kBN * 4);
         m0_restore(m0v);
         return n;
     };
@@ -780,20 +785,34 @@ void fwd_kernel(const FwdArgs args) {
         nS = __builtin_amdgcn_ballot_w64(ns);
         nM = __builtin_amdgcn_ballot_w64(nm);
     };
-    auto load_codes = [&](int kb0) { set_codes(ksum_at(kb0)); };
-    auto load_needs = [&](int kb0) { set_needs(ksum_at(kb0)); };
-    auto code_at = [&](int u, int sub) -> int {
-        return (int)((mb0[u] >> sub) & 1) | (int)(((mb1[u] >> sub) & 1) << 1) |
-               (int)(((mb2[u] >> sub) & 1) << 2);
+    // Control words of a window of 32 stages, one per lane (lane t: stage
+    // sw0 + t): the codes of the stage's two subtiles for each query block
+    // (3 bits each, block u from bit 6u) and, from bit 12, the tiles the stage
+    // copies. Built once per window, read with one readlane per stage. A
+    // rebuild's summary load waits for the copies in flight; windows move
+    // once per 32 stages.
+    int ctrl = 0, sw0 = 0;
+    auto build_ctrl = [&](int s0) {
+        sw0 = s0;
+        const int4 sm = ksum_at(2 * s0);  // lane: subtile 2*s0 + lane
+        set_codes(sm);
+        set_needs(sm);
+        const int t2 = 2 * (lane & 31);
+        int w = 0;
+#pragma unroll
+        for (int u = 0; u < QB; ++u) {
+            const int a = (int)((mb0[u] >> t2) & 1) | (int)(((mb1[u] >> t2) & 1) << 1) |
+                          (int)(((mb2[u] >> t2) & 1) << 2);
+            const int bb = (int)((mb0[u] >> (t2 + 1)) & 1) | (int)(((mb1[u] >> (t2 + 1)) & 1) << 1) |
+                           (int)(((mb2[u] >> (t2 + 1)) & 1) << 2);
+            w |= (a | bb << 3) << (6 * u);
+        }
+        const int tl = (((nS >> t2) & 3) != 0 ? 5 : 0) | (((nM >> t2) & 3) != 0 ? 10 : 0);
+        ctrl = w | tl << 12;
     };
 
     // ---- main loop over stages ----
-    int kbp = 0, kbi = 0;  // first subtile of the code / need windows
-    {
-        const int4 sm = ksum_at(0);
-        set_codes(sm);
-        set_needs(sm);
-    }
+    build_ctrl(0);
     // Every prologue load (Q, chain ids, summaries) and the stage-0 copy have
     // landed here. The compiler sees this wait (the copies are inline asm it
     // cannot see), so it adds no vmcnt(0) at later uses, which would also
@@ -803,20 +822,12 @@ void fwd_kernel(const FwdArgs args) {
     // Tiles stage t copies (bit i = tile i): K_self and V_self (bits 0, 2)
     // if any of its subtiles needs the self pathway, K_multi and V_multi
     // (1, 3) for the multimer pathway.
-    auto tiles_for = [&](int t) -> int {
-        if (2 * t + 1 - kbi >= 64) {
-            kbi = 2 * t;
-            load_needs(kbi);
-        }
-        const int nx = 2 * t - kbi;
-        const int m = (((nS >> nx) & 3) != 0 ? 5 : 0) | (((nM >> nx) & 3) != 0 ? 10 : 0);
-        return __builtin_amdgcn_readfirstlane(m);
-    };
+    auto tiles_of = [&](int t) -> int { return __builtin_amdgcn_readlane(ctrl, t - sw0) >> 12; };
     // pend[k]: vector-memory instructions of stage s + k still in flight
     // (stage 0 was issued before the prologue and has landed).
 #pragma unroll
     for (int t = 1; t < NBUF - 1; ++t)
-        if (t < nst) pend[t] = issue(t, t, tiles_for(t));
+        if (t < nst) pend[t] = issue(t, t, tiles_of(t));
     int bf = 0;
     for (int s = 0; s < nst; ++s) {
         int allow = 0;  // copies of later stages that may stay in flight
@@ -827,20 +838,17 @@ void fwd_kernel(const FwdArgs args) {
 #pragma unroll
         for (int k = 0; k < NBUF - 1; ++k) pend[k] = pend[k + 1];
         pend[NBUF - 1] = 0;
-        if (2 * s + 1 - kbp >= 64) {
-            kbp = 2 * s;
-            load_codes(kbp);
-        }
-        const int sub = 2 * s - kbp;
+        if (s + NBUF - 1 - sw0 >= 32) build_ctrl(s);
+        const int cw = __builtin_amdgcn_readlane(ctrl, s - sw0);
         int c0[QB], c1[QB];
 #pragma unroll
         for (int u = 0; u < QB; ++u) {
-            c0[u] = code_at(u, sub);
-            c1[u] = code_at(u, sub + 1);
+            c0[u] = (cw >> (6 * u)) & 7;
+            c1[u] = (cw >> (6 * u + 3)) & 7;
         }
         if (s + NBUF - 1 < nst) {
             const int bn = bf + NBUF - 1 >= NBUF ? bf - 1 : bf + NBUF - 1;
-            pend[NBUF - 2] = issue(s + NBUF - 1, bn, tiles_for(s + NBUF - 1));
+            pend[NBUF - 2] = issue(s + NBUF - 1, bn, tiles_of(s + NBUF - 1));
         }
 
         const char* stage = smem + bf * S::STAGE;
