@@ -51,7 +51,8 @@ inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
 // Workspace layout (offsets 256-byte aligned):
 //   keff int32 [B][Lp]          effective chain id per key
-//   ksum int32 [B][Lp/32][4]    keys: min chain, max chain (valid keys), #padded, 0
+//   ksum int32 [B][Lp/32][4]    keys: min chain, max chain (valid keys), #padded,
+//                               1 if the padded keys are a suffix of the 32
 //   qsum int32 [B][Lp/32][4]    queries: min chain, max chain (queries < L), 0, 0
 //   krot T     [B][H][Lp][D]    RoPE-rotated K_self (fused RoPE only)
 struct FwdWs {
@@ -116,8 +117,11 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p
             int* o = ksum + blk * 4;
             o[0] = mn;
             o[1] = mx;
-            o[2] = __popcll(hh ? (padm >> 32) : (padm & 0xffffffffull));
-            o[3] = 0;
+            const unsigned pm = (unsigned)(hh ? (padm >> 32) : (padm & 0xffffffffull));
+            const int np = __popc(pm);
+            o[2] = np;
+            // 1 when the padded keys are the last np keys of the 32
+            o[3] = (np > 0 && np < 32 && pm == (0xffffffffu << (32 - np))) ? 1 : 0;
             int* oq = qsum + blk * 4;
             oq[0] = qmn;
             oq[1] = qmx;
@@ -673,18 +677,19 @@ void fwd_kernel(const FwdArgs args) {
 
     // One subtile of block u on the slow path. code: 0 pure self, 1 pure
     // multimer, 2 straddle (keys on one chain, queries on several: pathway per
-    // lane), 3 general, 4 skip.
+    // lane), 3 general, 4 skip, 5 / 6 pure self / multimer with padded keys.
     auto slow_subtile = [&](auto u_c, const char* stage, const int* cid, int st, int code, int k0) {
         constexpr int u = decltype(u_c)::value;
-        if (code >= 4) return;
+        if (code == 4) return;
         if (code == 3) {
             general(u_c, stage, cid, st, k0);
             return;
         }
         v8 pb[1][2];
         float ls;
-        if (code <= 1) {
-            const int pw = code;
+        if (code <= 1 || code >= 5) {
+            const bool masked = code >= 5;
+            const int pw = masked ? code - 5 : code;
             const char* kt = stage + pw * S::TILE;
             v8 qa[S::NKK];
 #pragma unroll
@@ -694,6 +699,19 @@ void fwd_kernel(const FwdArgs args) {
 #pragma unroll
                 for (int kk = 0; kk < S::NKK; ++kk) kr[kk] = kop_t(kt, st, kk);
                 sv[0] = qkq(kr, qa);
+                if (masked) {
+#pragma unroll
+                    for (int cc = 0; cc < 2; ++cc) {
+                        const int kl = st * 32 + 16 * cc + 8 * hh;
+                        const i32x4 k0v = *reinterpret_cast<const i32x4*>(&cid[kl]);
+                        const i32x4 k1v = *reinterpret_cast<const i32x4*>(&cid[kl + 4]);
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) {
+                            const int ck = t < 4 ? k0v[t & 3] : k1v[t & 3];
+                            if (ck == kPadChain) sv[0][8 * cc + t] = -INFINITY;
+                        }
+                    }
+                }
             };
             {
                 f32x16 sv[1];
@@ -741,12 +759,15 @@ void fwd_kernel(const FwdArgs args) {
         }
     };
 
-    auto subtile_mode = [&](int kmin, int kmax, int npad, int qmin, int qmax) -> int {
+    // Codes 5 / 6: pure self / multimer subtile whose padded keys are a
+    // suffix (the padding tail): one pathway with the padded keys masked.
+    auto subtile_mode = [&](int kmin, int kmax, int npad, int suffix, int qmin, int qmax) -> int {
         if (npad == 32) return 4;
         if (DENSE) return 3;
-        if (npad == 0) {
-            if (kmax < qmin || kmin > qmax) return 1;
-            if (kmin == kmax) return qmin == qmax ? 0 : 2;
+        if (npad == 0 || suffix) {
+            if (kmax < qmin || kmin > qmax) return npad ? 6 : 1;
+            if (kmin == kmax && qmin == qmax) return npad ? 5 : 0;
+            if (kmin == kmax && npad == 0) return 2;
         }
         return 3;
     };
@@ -766,7 +787,7 @@ void fwd_kernel(const FwdArgs args) {
     auto set_codes = [&](const int4 sm) {
 #pragma unroll
         for (int u = 0; u < QB; ++u) {
-            const int code = subtile_mode(sm.x, sm.y, sm.z, cq_min[u], cq_max[u]);
+            const int code = subtile_mode(sm.x, sm.y, sm.z, sm.w, cq_min[u], cq_max[u]);
             mb0[u] = __builtin_amdgcn_ballot_w64(code & 1);
             mb1[u] = __builtin_amdgcn_ballot_w64((code >> 1) & 1);
             mb2[u] = __builtin_amdgcn_ballot_w64((code >> 2) & 1);
