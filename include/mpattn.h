@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MPATTN_VERSION 2
+#define MPATTN_VERSION 3
 
 enum {
     MPATTN_OK = 0,
@@ -90,10 +90,12 @@ typedef struct mpattn_fwd_params {
     int32_t rope;            /* MPATTN_ROPE_NONE / MPATTN_ROPE_FUSED         */
     float scale;             /* logit scale (> 0), e.g. D^-1/2               */
     int32_t sqrt_softmax;    /* 1: O = sum sqrt(P) V (muS variant)           */
-    float dropout_p;         /* must be 0                                    */
+    float dropout_p;         /* attention dropout in [0, 1); > 0 needs 16-bit
+                                inputs and sqrt_softmax == 0               */
     void *workspace;         /* >= mpattn_fwd_workspace_size() bytes, 16-byte
                                 aligned; contents need no initialisation   */
     int64_t workspace_bytes;
+    uint64_t dropout_seed;   /* seed of the dropout mask (see below)         */
 } mpattn_fwd_params;
 
 typedef struct mpattn_bwd_params {
@@ -112,7 +114,19 @@ typedef struct mpattn_bwd_params {
     int32_t dtype, rope;
     float scale;
     int32_t sqrt_softmax;
+    float dropout_p;          /* the forward's dropout_p and dropout_seed    */
+    uint64_t dropout_seed;
 } mpattn_bwd_params;
+
+/* Attention dropout. Element (b, h, i, j) of P is kept, and scaled by
+ * 1 / (1 - dropout_p), when
+ *   r = fmix32(fmix32(lo ^ (b*H + h) * 0xC2B2AE3D ^ i * 0x9E3779B1)
+ *              ^ (j * 0x85EBCA77 + hi))
+ * has (r >> 8) >= round(dropout_p * 2^24), with lo / hi the low / high 32 bits
+ * of dropout_seed and fmix32 the MurmurHash3 32-bit finaliser (x ^= x >> 16;
+ * x *= 0x85EBCA6B; x ^= x >> 13; x *= 0xC2B2AE35; x ^= x >> 16), all in
+ * unsigned 32-bit arithmetic. The row sums of the softmax use P before
+ * dropout. The backward with the same seed regenerates the mask. */
 
 /* Workspace bytes mpattn_fwd needs (chain-id staging; RoPE-rotated K_self
  * when rope == MPATTN_ROPE_FUSED). */

@@ -61,6 +61,7 @@ class FwdParams(ctypes.Structure):
         ("scale", ctypes.c_float), ("sqrt_softmax", ctypes.c_int32),
         ("dropout_p", ctypes.c_float),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+        ("dropout_seed", ctypes.c_uint64),
     ]
 
 
@@ -81,6 +82,7 @@ class BwdParams(ctypes.Structure):
         ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("L", ctypes.c_int32), ("D", ctypes.c_int32),
         ("dtype", ctypes.c_int32), ("rope", ctypes.c_int32),
         ("scale", ctypes.c_float), ("sqrt_softmax", ctypes.c_int32),
+        ("dropout_p", ctypes.c_float), ("dropout_seed", ctypes.c_uint64),
     ]
 
 
@@ -278,11 +280,13 @@ def _aligned(t):
 
 def mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, *, chain_ids=None,
                chain_mask=None, key_padding_mask=None, rope=False, scale=1.0,
-               sqrt_softmax=False, dropout_p=0.0, out=None, need_lse=False):
+               sqrt_softmax=False, dropout_p=0.0, dropout_seed=0, out=None, need_lse=False):
     """Launch the forward kernel on the current stream.
 
     Returns ``out`` (B, H, L, D) and, if ``need_lse``, the fp32 (B, H, L)
-    log-sum-exp (natural units of the scaled logits).
+    log-sum-exp (natural units of the scaled logits). With ``dropout_p`` > 0
+    the keep mask is a function of ``dropout_seed`` (a 64-bit integer) and the
+    element's (b, h, query, key); the LSE is that of the undropped softmax.
     """
     ins = [q_self, k_self, v_self, q_multi, k_multi, v_multi]
     names = ["q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi"]
@@ -312,6 +316,7 @@ def mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, *, chain_ids=N
     p.scale = float(scale)
     p.sqrt_softmax = 1 if sqrt_softmax else 0
     p.dropout_p = float(dropout_p)
+    p.dropout_seed = int(dropout_seed) & 0xFFFFFFFFFFFFFFFF
     lib = load_library()
     ws_bytes = lib.mpattn_fwd_workspace_size(B, H, L, D, p.dtype, p.rope)
     if ws_bytes < 0:
@@ -327,8 +332,11 @@ def mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, *, chain_ids=N
 
 def mpattn_bwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, out, lse, grad_out, *,
                chain_ids=None, chain_mask=None, key_padding_mask=None, rope=False, scale=1.0,
-               sqrt_softmax=False, grads=None):
+               sqrt_softmax=False, dropout_p=0.0, dropout_seed=0, grads=None):
     """Launch the backward kernels; returns (dq_s, dk_s, dv_s, dq_m, dk_m, dv_m).
+
+    ``dropout_p`` / ``dropout_seed`` must be the forward's: the keep mask is
+    regenerated from them.
 
     ``grads`` optionally supplies the six (B, H, L, D) output views (any
     strides the ABI accepts, e.g. slices of one projection-gradient buffer);
@@ -371,6 +379,8 @@ def mpattn_bwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, out, lse, grad
     p.rope = MPATTN_ROPE_FUSED if rope else MPATTN_ROPE_NONE
     p.scale = float(scale)
     p.sqrt_softmax = 1 if sqrt_softmax else 0
+    p.dropout_p = float(dropout_p)
+    p.dropout_seed = int(dropout_seed) & 0xFFFFFFFFFFFFFFFF
     rc = lib.mpattn_bwd(ctypes.byref(p), _stream_handle(dev))
     _check(rc, "mpattn_bwd")
     del keep, ins

@@ -78,6 +78,16 @@ int check_common(int B, int H, int L, int D, int dtype, int rope, float scale,
     return MPATTN_OK;
 }
 
+// Attention dropout: p in [0, 1); p > 0 is built for the 16-bit softmax
+// kernels only.
+int check_dropout(float p, int dtype, int sqrt_softmax) {
+    if (!(p >= 0.f && p < 1.f)) return fail(MPATTN_ERR_INVALID, "dropout_p must be in [0, 1) (got %g)", (double)p);
+    if (p > 0.f && dtype == MPATTN_FP32)
+        return fail(MPATTN_ERR_UNSUPPORTED, "dropout_p > 0 needs bf16 or fp16 inputs");
+    if (p > 0.f && sqrt_softmax) return fail(MPATTN_ERR_UNSUPPORTED, "dropout_p > 0 with sqrt_softmax is not built");
+    return MPATTN_OK;
+}
+
 // Shape, dtype and mask checks shared by the combine entry points.
 int check_combine(int B, int H, int L, int D, int dtype, const uint8_t* mask, int64_t msb,
                   int64_t msq, int64_t msk, float dropout_p) {
@@ -120,8 +130,7 @@ int mpattn_fwd(const mpattn_fwd_params* p, void* stream) {
                           p->chain_mask, p->mask_stride_b, p->mask_stride_q, p->mask_stride_k,
                           p->rope_cos, p->rope_sin, p->sqrt_softmax);
     if (rc) return rc;
-    if (p->dropout_p != 0.f)
-        return fail(MPATTN_ERR_UNSUPPORTED, "dropout_p must be 0 (got %g)", (double)p->dropout_p);
+    if ((rc = check_dropout(p->dropout_p, p->dtype, p->sqrt_softmax))) return rc;
     const int es = elt_size(p->dtype);
     const mpattn_tensor* ts[7] = {&p->q_self, &p->k_self, &p->v_self, &p->q_multi,
                                   &p->k_multi, &p->v_multi, &p->out};
@@ -168,6 +177,7 @@ int mpattn_bwd(const mpattn_bwd_params* p, void* stream) {
                           p->chain_mask, p->mask_stride_b, p->mask_stride_q, p->mask_stride_k,
                           p->rope_cos, p->rope_sin, p->sqrt_softmax);
     if (rc) return rc;
+    if ((rc = check_dropout(p->dropout_p, p->dtype, p->sqrt_softmax))) return rc;
     const int es = elt_size(p->dtype);
     const mpattn_tensor* ts[14] = {&p->q_self,  &p->k_self,   &p->v_self,  &p->q_multi, &p->k_multi,
                                    &p->v_multi, &p->out,      &p->grad_out, &p->dq_self, &p->dk_self,

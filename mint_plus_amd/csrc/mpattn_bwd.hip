@@ -8,6 +8,8 @@
 //   dV_j  = sum_i P_ij dO_i                  (into V_self or V_multi by pathway)
 //   dP_ij = dO_i . V_sel(ij),j
 //   dS_ij = P_ij (dP_ij - Delta_i),           Delta_i = dO_i . O_i
+//   with dropout (keep mask Z, r = 1/(1-p), regenerated from the seed):
+//   dV_j = r sum_i Z_ij P_ij dO_i,  dP_ij = r Z_ij dO_i . V_sel(ij),j
 //   dQ_i  = scale sum_j dS_ij K_sel,j ;  dK_j = scale sum_i dS_ij Q_sel,i
 //   and R_p^T applied to dQ_self / dK_self with fused RoPE.
 //
@@ -86,6 +88,7 @@ struct BwdArgs {
     int Lp;
     float c;     // logit factor: scale * log2(e), halved for sqrt-softmax
     float lmul;  // LSE factor: log2(e), halved for sqrt-softmax
+    DropCfg drop;
 };
 
 // ---------------------------------------------------------------------------
@@ -266,7 +269,7 @@ __device__ void store_rows(const f32x16* acc, float* scratch, const mpattn_tenso
 // ---------------------------------------------------------------------------
 // dK / dV: key-stationary.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT>
+template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     using TS = TileShape<D>;
     using BS = BwdShape<D>;
@@ -469,6 +472,20 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
         for (int kk = 0; kk < BS::NKK; ++kk) doa[kk] = rop(stage, 2, st, kk);
         f32x16 pm, dsm;  // P and dS in the selected pathway, per slot
         bool same[16];
+        // Dropout: dP of dropped entries is 0, kept ones scaled by 1/(1-p);
+        // the dV operand is Z*P (the 1/(1-p) goes into the dV store).
+        bool keep[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) keep[i] = true;
+        if constexpr (DROP) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int qg = q0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8);
+                keep[i] = drop_keep(drop_row(a.drop.lo, (uint32_t)bh, (uint32_t)qg), a.drop.hi, (uint32_t)key,
+                                    a.drop.thr);
+            }
+        }
+        auto dpe = [&](float dp, int i) { return DROP ? (keep[i] ? dp * a.drop.rkeep : 0.f) : dp; };
         if (mode != 2) {
             const int pw = mode;
 #pragma unroll
@@ -478,7 +495,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 pm[i] = fast_exp2(fmaf(sv[i], c, -l2[i]));
-                dsm[i] = dscore(pm[i], dp[i], dl[i]);
+                dsm[i] = dscore(pm[i], dpe(dp[i], i), dl[i]);
                 same[i] = pw == 0;
             }
         } else {
@@ -513,7 +530,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
                 const float s = sm_ ? ss[i] : sm[i];
                 const float dp = sm_ ? dps[i] : dpm[i];
                 pm[i] = kvalid ? fast_exp2(fmaf(s, c, -l2[i])) : 0.f;
-                dsm[i] = dscore(pm[i], dp, dl[i]);
+                dsm[i] = dscore(pm[i], dpe(dp, i), dl[i]);
             }
         }
         // dV_pw += P^T dO ; dK_pw += dS^T Q_pw, per 16-query chunk cc
@@ -523,7 +540,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 const int i = 8 * cc + t;
-                const T pv = (T)pm[i], dv_ = (T)dsm[i];
+                const T pv = (T)(keep[i] ? pm[i] : 0.f), dv_ = (T)dsm[i];
                 ps[t] = same[i] ? pv : (T)0.f;
                 pmv[t] = same[i] ? (T)0.f : pv;
                 dss[t] = same[i] ? dv_ : (T)0.f;
@@ -579,8 +596,9 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
 
     float* scratch = (float*)(smem + wave * 32 * 65 * 4);
     const float scale = p.scale;
-    store_rows<T, D, false>(dv[0], scratch, p.dv_self, b, h, kw0, L, 1.0f, false, nullptr, nullptr);
-    store_rows<T, D, false>(dv[1], scratch, p.dv_multi, b, h, kw0, L, 1.0f, false, nullptr, nullptr);
+    const float vmul = DROP ? a.drop.rkeep : 1.0f;
+    store_rows<T, D, false>(dv[0], scratch, p.dv_self, b, h, kw0, L, vmul, false, nullptr, nullptr);
+    store_rows<T, D, false>(dv[1], scratch, p.dv_multi, b, h, kw0, L, vmul, false, nullptr, nullptr);
     store_rows<T, D, false>(dk[0], scratch, p.dk_self, b, h, kw0, L, scale, ROPE, p.rope_cos, p.rope_sin);
     store_rows<T, D, false>(dk[1], scratch, p.dk_multi, b, h, kw0, L, scale, false, nullptr, nullptr);
 }
@@ -588,7 +606,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
 // ---------------------------------------------------------------------------
 // dQ: query-stationary.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT>
+template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     using TS = TileShape<D>;
     using BS = BwdShape<D>;
@@ -649,6 +667,13 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
         dof[kk] = pack8<T>(x);
     }
     const float l2 = qin ? a.lse2[(int64_t)bh * Lp + q] : INFINITY;
+    const uint32_t drow = DROP ? drop_row(a.drop.lo, (uint32_t)bh, (uint32_t)q) : 0u;
+    // dP of dropped entries is 0, kept ones scaled by 1/(1-p); key of slot i
+    // of subtile st: k0 + st*32 + 16*(i/8) + 8*hh + i%8.
+    auto dpe = [&](float dp, int kg) {
+        if constexpr (!DROP) return dp;
+        return drop_keep(drow, a.drop.hi, (uint32_t)kg, a.drop.thr) ? dp * a.drop.rkeep : 0.f;
+    };
     const float dl = qin ? a.delta[(int64_t)bh * Lp + q] : 0.f;
     int cq = 0, cq_min = 0, cq_max = 0;
     const uint8_t* mrow = nullptr;
@@ -781,7 +806,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const float pv = fast_exp2(fmaf(sv[i], c, -l2));
-                dsv[i] = dscore(pv, dp[i], dl);
+                dsv[i] = dscore(pv, dpe(dp[i], k0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8)), dl);
                 same[i] = pw == 0;
             }
         } else {
@@ -817,7 +842,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
                     const float s = sm_ ? ss[i] : sm[i];
                     const float dp = sm_ ? dps[i] : dpm[i];
                     const float pv = ck == kPadChain ? 0.f : fast_exp2(fmaf(s, c, -l2));
-                    dsv[i] = dscore(pv, dp, dl);
+                    dsv[i] = dscore(pv, dpe(dp, k0 + kl + t), dl);
                 }
             }
         }
@@ -879,7 +904,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool ROPE, bool DENSE, bool SQRT>
+template <typename T, int D, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     constexpr int W = 4;
     BwdArgs a;
@@ -888,6 +913,7 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     a.Lp = Lp;
     a.c = p.scale * kLog2e * (SQRT ? 0.5f : 1.0f);
     a.lmul = kLog2e * (SQRT ? 0.5f : 1.0f);
+    a.drop = drop_cfg(p.dropout_p, p.dropout_seed);
     const BwdWs ws = bwd_ws_layout(p.B, p.H, p.L, D, sizeof(T), ROPE);
     char* w = (char*)p.workspace;
     float* lse2 = (float*)(w + ws.lse2);
@@ -915,9 +941,9 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     if (e != hipSuccess) return e;
     const int nb = (p.L + 32 * W - 1) / (32 * W);
     const unsigned grid = (unsigned)((int64_t)p.B * p.H * nb);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, DENSE, SQRT>), dim3(grid), dim3(W * 64), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(grid), dim3(W * 64), 0, stream, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, DENSE, SQRT>), dim3(grid), dim3(W * 64), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(grid), dim3(W * 64), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -925,12 +951,16 @@ template <typename T, int D>
 static hipError_t dispatch_bwd_d(const mpattn_bwd_params& p, hipStream_t s) {
     const bool rope = p.rope == MPATTN_ROPE_FUSED;
     const bool dense = p.chain_mask != nullptr;
-    if (p.sqrt_softmax) {
-        if (rope) return dense ? launch_bwd_t<T, D, true, true, true>(p, s) : launch_bwd_t<T, D, true, false, true>(p, s);
-        return dense ? launch_bwd_t<T, D, false, true, true>(p, s) : launch_bwd_t<T, D, false, false, true>(p, s);
+    if (p.sqrt_softmax) {  // (dropout with sqrt-softmax is rejected by the API)
+        if (rope) return dense ? launch_bwd_t<T, D, true, true, true, false>(p, s) : launch_bwd_t<T, D, true, false, true, false>(p, s);
+        return dense ? launch_bwd_t<T, D, false, true, true, false>(p, s) : launch_bwd_t<T, D, false, false, true, false>(p, s);
     }
-    if (rope) return dense ? launch_bwd_t<T, D, true, true, false>(p, s) : launch_bwd_t<T, D, true, false, false>(p, s);
-    return dense ? launch_bwd_t<T, D, false, true, false>(p, s) : launch_bwd_t<T, D, false, false, false>(p, s);
+    if (p.dropout_p > 0.f) {
+        if (rope) return dense ? launch_bwd_t<T, D, true, true, false, true>(p, s) : launch_bwd_t<T, D, true, false, false, true>(p, s);
+        return dense ? launch_bwd_t<T, D, false, true, false, true>(p, s) : launch_bwd_t<T, D, false, false, false, true>(p, s);
+    }
+    if (rope) return dense ? launch_bwd_t<T, D, true, true, false, false>(p, s) : launch_bwd_t<T, D, true, false, false, false>(p, s);
+    return dense ? launch_bwd_t<T, D, false, true, false, false>(p, s) : launch_bwd_t<T, D, false, false, false, false>(p, s);
 }
 
 template <typename T>

@@ -183,6 +183,38 @@ __device__ __forceinline__ typename Elt<T>::v8 pack8(const float x[8]) {
     return r;
 }
 
+// Attention dropout mask (the definition is in mpattn.h): per-row hash of
+// (seed low word, b*H + h, query i), then per element the keep test for key j.
+__device__ __forceinline__ uint32_t fmix32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x85EBCA6Bu;
+    x ^= x >> 13;
+    x *= 0xC2B2AE35u;
+    x ^= x >> 16;
+    return x;
+}
+__device__ __forceinline__ uint32_t drop_row(uint32_t lo, uint32_t bh, uint32_t i) {
+    return fmix32(lo ^ (bh * 0xC2B2AE3Du) ^ (i * 0x9E3779B1u));
+}
+__device__ __forceinline__ bool drop_keep(uint32_t row, uint32_t hi, uint32_t j, uint32_t thr) {
+    return (fmix32(row ^ (j * 0x85EBCA77u + hi)) >> 8) >= thr;
+}
+
+// Dropout constants of a call: seed words, the 24-bit drop threshold and the
+// keep scale 1 / (1 - p).
+struct DropCfg {
+    uint32_t lo, hi, thr;
+    float rkeep;
+};
+inline DropCfg drop_cfg(float p, uint64_t seed) {
+    DropCfg d;
+    d.lo = (uint32_t)seed;
+    d.hi = (uint32_t)(seed >> 32);
+    d.thr = (uint32_t)((double)p * 16777216.0 + 0.5);
+    d.rkeep = p > 0.f ? 1.0f / (1.0f - p) : 1.0f;
+    return d;
+}
+
 // LDS byte address of a __shared__ object.
 __device__ __forceinline__ unsigned lds_addr(const void* ptr) {
     return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;

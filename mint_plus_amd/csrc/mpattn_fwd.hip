@@ -85,6 +85,7 @@ struct FwdArgs {
     int Lp;
     float qmul;    // factor applied to q while loading (scale*log2e when fused, else 1)
     float c;       // base-2 factor applied to raw logits (1 when fused)
+    DropCfg drop;  // attention dropout (DROP kernels)
 };
 
 // ---------------------------------------------------------------------------
@@ -227,7 +228,9 @@ template <int N, typename F> __device__ __forceinline__ void for_blocks(F&& f) {
 // SQRT: sqrt-softmax, O = sum_j sqrt(P_ij) V_j. The kernel then works with
 // e = exp2(s2 / 2) (the 1/2 is folded into the logit factor), accumulates
 // sum e V and sum e^2, and divides by sqrt(sum e^2) at the end.
-template <typename T, int D, int W, int QB, int WPE, int NBUF, bool ROPE, bool DENSE, bool SQRT>
+// DROP: attention dropout; the PV operand takes the kept probabilities, the
+// row sums all of them, and O is scaled by 1 / (1 - p) at the end.
+template <typename T, int D, int W, int QB, int WPE, int NBUF, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void fwd_kernel(const FwdArgs args) {
     using S = FwdShape<D>;
@@ -264,6 +267,9 @@ void fwd_kernel(const FwdArgs args) {
         qrow[u] = qv0 + 32 * u + ql;
         qvalid[u] = qrow[u] < L;
     }
+    uint32_t drow[QB];  // dropout row hashes
+#pragma unroll
+    for (int u = 0; u < QB; ++u) drow[u] = DROP ? drop_row(args.drop.lo, (uint32_t)bh, (uint32_t)qrow[u]) : 0u;
 
     auto base = [&](const mpattn_tensor& t) {
         return (const T*)t.ptr + b * t.stride_b + h * t.stride_h;
@@ -287,7 +293,7 @@ void fwd_kernel(const FwdArgs args) {
     unsigned dinc[NJ];    // bytes between stages: 64 rows (uniform)
     unsigned dlds[NJ];    // LDS offset inside a stage (uniform)
     const char* dva[NJ];  // per-lane source address of (r, c) in stage 0
-    int drow[NJ], dcol[NJ];
+    int drw[NJ], dcol[NJ];
     int dten[NJ];         // tile index, 4 for an idle copy (uniform)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -303,7 +309,7 @@ void fwd_kernel(const FwdArgs args) {
         dstr[j] = (unsigned)(ts * (int64_t)sizeof(T));
         dinc[j] = dstr[j] * kBN;
         dlds[j] = ten * S::TILE + part * 1024;
-        drow[j] = r;
+        drw[j] = r;
         dcol[j] = cb;
         dva[j] = dsb[j] + (r * dstr[j] + cb);
         dten[j] = ins0 < TOT ? ten : 4;
@@ -325,7 +331,7 @@ void fwd_kernel(const FwdArgs args) {
             for (int j = 0; j < NJ; ++j) va[j] = dva[j] + (unsigned)s * dinc[j];
         } else {  // last stage: clamp rows past L to L-1 (their keys are masked)
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) va[j] = dsb[j] + ((unsigned)min(k0 + drow[j], L - 1) * dstr[j] + dcol[j]);
+            for (int j = 0; j < NJ; ++j) va[j] = dsb[j] + ((unsigned)min(k0 + drw[j], L - 1) * dstr[j] + dcol[j]);
         }
         const int m0v = m0_save();
         int n = 1;
@@ -466,7 +472,10 @@ void fwd_kernel(const FwdArgs args) {
     };
     // Probabilities of NS subtiles (slot 8*cc + t -> pb[st][cc][t]) and their
     // row sum over this lane's keys.
-    auto probs = [&](auto ns_c, const f32x16* sv, v8 (*pb)[2], bool sh, float mr) -> float {
+    // kb: key of slot 0 of the first subtile (slot 8*cc + t of subtile st is
+    // key kb + 32*st + 16*cc + t); dr: the block's dropout row hash.
+    auto probs = [&](auto ns_c, const f32x16* sv, v8 (*pb)[2], bool sh, float mr, int kb,
+                     uint32_t dr) -> float {
         constexpr int NS = decltype(ns_c)::value;
         typedef float f32x2 __attribute__((ext_vector_type(2)));
         // Pairs are rounded once (v_cvt_pk) and feed both the PV operand and
@@ -483,8 +492,21 @@ void fwd_kernel(const FwdArgs args) {
                                      prob(sv[st][8 * cc + 2 * uu + 1], sh, mr)};
                     pr[uu] = __builtin_convertvector(f, v2);
                 }
-                pb[st][cc] = __builtin_shufflevector(__builtin_shufflevector(pr[0], pr[1], 0, 1, 2, 3),
-                                                     __builtin_shufflevector(pr[2], pr[3], 0, 1, 2, 3), 0, 1, 2,
+                v2 pv[4];
+#pragma unroll
+                for (int uu = 0; uu < 4; ++uu) pv[uu] = pr[uu];
+                if constexpr (DROP) {
+                    const int kj = kb + 32 * st + 16 * cc;
+#pragma unroll
+                    for (int uu = 0; uu < 4; ++uu) {
+                        const bool k0 = drop_keep(dr, args.drop.hi, (uint32_t)(kj + 2 * uu), args.drop.thr);
+                        const bool k1 = drop_keep(dr, args.drop.hi, (uint32_t)(kj + 2 * uu + 1), args.drop.thr);
+                        const uint32_t m = (k0 ? 0x0000FFFFu : 0u) | (k1 ? 0xFFFF0000u : 0u);
+                        pv[uu] = __builtin_bit_cast(v2, __builtin_bit_cast(uint32_t, pr[uu]) & m);
+                    }
+                }
+                pb[st][cc] = __builtin_shufflevector(__builtin_shufflevector(pv[0], pv[1], 0, 1, 2, 3),
+                                                     __builtin_shufflevector(pv[2], pv[3], 0, 1, 2, 3), 0, 1, 2,
                                                      3, 4, 5, 6, 7);
                 if constexpr (SQRT) {
                     ls0 = E::sq2(pr[0], ls0);
@@ -504,7 +526,7 @@ void fwd_kernel(const FwdArgs args) {
     // nothing yet. The subtile's logits are recomputed from LDS (`logits`
     // fills sv) and its probabilities redone relative to a reference max
     // taken from them (raised only, once something has been accumulated).
-    auto fixup = [&](auto u_c, auto logits, v8 (*pb)[2]) -> float {
+    auto fixup = [&](auto u_c, auto logits, v8 (*pb)[2], int kb) -> float {
         constexpr int u = decltype(u_c)::value;
         f32x16 sv[1];
         logits(sv);
@@ -525,7 +547,7 @@ void fwd_kernel(const FwdArgs args) {
             for (int i = 0; i < 16; ++i) o[u][db][i] *= alpha;
         m_ref[u] = m_new;
         shifted[u] = __builtin_amdgcn_ballot_w64(m_new != 0.f) != 0;
-        return probs(IC<1>{}, sv, pb, true, m_new);
+        return probs(IC<1>{}, sv, pb, true, m_new, kb, drow[u]);
     };
     // Check: true if any lane of block u needs the fix-up.
     auto needs_fix = [&](float ls, float lr) {
@@ -571,7 +593,7 @@ void fwd_kernel(const FwdArgs args) {
     // cores work on block u+1 while the VALU does block u's softmax. Returns
     // the mask of blocks accumulated; a block that needs the fix-up is left
     // to the slow path.
-    auto fast_stage = [&](const char* stage, int pw) -> int {
+    auto fast_stage = [&](const char* stage, int pw, int k0) -> int {
         const char* kt = stage + pw * S::TILE;
         const char* vt = stage + (2 + pw) * S::TILE;
         // All LDS operands are read up front: the V reads overlap the softmax.
@@ -597,7 +619,7 @@ void fwd_kernel(const FwdArgs args) {
         for_blocks<QB>([&](auto u_c) {
             constexpr int u = decltype(u_c)::value;
             v8 pb[2][2];
-            const float ls = probs(IC<2>{}, sv[u], pb, false, 0.f);
+            const float ls = probs(IC<2>{}, sv[u], pb, false, 0.f, k0 + 8 * hh, drow[u]);
             if (needs_fix(ls, l_run[u])) return;
             l_run[u] += ls;
             done |= 1 << u;
@@ -615,6 +637,7 @@ void fwd_kernel(const FwdArgs args) {
     // padded keys.
     auto general = [&](auto u_c, const char* stage, const int* cid, int st, int k0) {
         constexpr int u = decltype(u_c)::value;
+        const int kbs = k0 + 32 * st + 8 * hh;
         bool same[16];
         // Selected raw logits (-inf for padded keys) into sv[0]; keys of
         // slot i: st*32 + 16*(i/8) + 8*hh + i%8.
@@ -654,9 +677,10 @@ void fwd_kernel(const FwdArgs args) {
         {
             f32x16 sv[1];
             logits(sv);
-            ls = shifted[u] ? probs(IC<1>{}, sv, pb, true, m_ref[u]) : probs(IC<1>{}, sv, pb, false, 0.f);
+            ls = shifted[u] ? probs(IC<1>{}, sv, pb, true, m_ref[u], kbs, drow[u])
+                            : probs(IC<1>{}, sv, pb, false, 0.f, kbs, drow[u]);
         }
-        if (needs_fix(ls, l_run[u])) ls = fixup(u_c, logits, pb);
+        if (needs_fix(ls, l_run[u])) ls = fixup(u_c, logits, pb, kbs);
         l_run[u] += ls;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
@@ -680,6 +704,7 @@ void fwd_kernel(const FwdArgs args) {
     // lane), 3 general, 4 skip, 5 / 6 pure self / multimer with padded keys.
     auto slow_subtile = [&](auto u_c, const char* stage, const int* cid, int st, int code, int k0) {
         constexpr int u = decltype(u_c)::value;
+        const int kbs = k0 + 32 * st + 8 * hh;
         if (code == 4) return;
         if (code == 3) {
             general(u_c, stage, cid, st, k0);
@@ -716,9 +741,10 @@ void fwd_kernel(const FwdArgs args) {
             {
                 f32x16 sv[1];
                 logits(sv);
-                ls = shifted[u] ? probs(IC<1>{}, sv, pb, true, m_ref[u]) : probs(IC<1>{}, sv, pb, false, 0.f);
+                ls = shifted[u] ? probs(IC<1>{}, sv, pb, true, m_ref[u], kbs, drow[u])
+                                : probs(IC<1>{}, sv, pb, false, 0.f, kbs, drow[u]);
             }
-            if (needs_fix(ls, l_run[u])) ls = fixup(u_c, logits, pb);
+            if (needs_fix(ls, l_run[u])) ls = fixup(u_c, logits, pb, kbs);
             l_run[u] += ls;
             const char* vt = stage + (2 + pw) * S::TILE;
 #pragma unroll
@@ -743,9 +769,10 @@ void fwd_kernel(const FwdArgs args) {
         {
             f32x16 sv[1];
             logits(sv);
-            ls = shifted[u] ? probs(IC<1>{}, sv, pb, true, m_ref[u]) : probs(IC<1>{}, sv, pb, false, 0.f);
+            ls = shifted[u] ? probs(IC<1>{}, sv, pb, true, m_ref[u], kbs, drow[u])
+                            : probs(IC<1>{}, sv, pb, false, 0.f, kbs, drow[u]);
         }
-        if (needs_fix(ls, l_run[u])) ls = fixup(u_c, logits, pb);
+        if (needs_fix(ls, l_run[u])) ls = fixup(u_c, logits, pb, kbs);
         l_run[u] += ls;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
@@ -886,7 +913,7 @@ void fwd_kernel(const FwdArgs args) {
 #pragma unroll
                     for (int kk = 0; kk < S::NKK; ++kk) qcur[u][kk] = cur_pw ? qf[u][1][kk] : qf[u][0][kk];
             }
-            done = fast_stage(stage, c0[0]);
+            done = fast_stage(stage, c0[0], s * kBN);
         }
         if (done != (1 << QB) - 1) {
             const int* cid = &scid[wave][bf][0];
@@ -905,7 +932,8 @@ void fwd_kernel(const FwdArgs args) {
 #pragma unroll
     for (int u = 0; u < QB; ++u) {
         const float l_tot = l_run[u] + __shfl_xor(l_run[u], 32);
-        const float inv = l_tot > 0.f ? (SQRT ? __frsqrt_rn(l_tot) : 1.0f / l_tot) : 0.f;
+        float inv = l_tot > 0.f ? (SQRT ? __frsqrt_rn(l_tot) : 1.0f / l_tot) : 0.f;
+        if constexpr (DROP) inv *= args.drop.rkeep;
         if (qvalid[u]) {
             T* orow = (T*)p.out.ptr + b * p.out.stride_b + h * p.out.stride_h + (int64_t)qrow[u] * p.out.stride_t;
 #pragma unroll
@@ -928,7 +956,7 @@ void fwd_kernel(const FwdArgs args) {
     }
 }
 
-template <typename T, int D, bool ROPE, bool DENSE, bool SQRT>
+template <typename T, int D, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     using C = FwdCfg<D>;
     constexpr int NBUF = D == 64 ? 2 : MPATTN_FWD_NBUF;
@@ -954,7 +982,7 @@ static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     const int nqb = (p.L + 32 * C::QB * C::W - 1) / (32 * C::QB * C::W);
     const int64_t grid = (int64_t)p.B * p.H * nqb;
-    hipLaunchKernelGGL((fwd_kernel<T, D, C::W, C::QB, C::WPE, NBUF, ROPE, DENSE, SQRT>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((fwd_kernel<T, D, C::W, C::QB, C::WPE, NBUF, ROPE, DENSE, SQRT, DROP>), dim3((unsigned)grid),
                        dim3(C::W * 64), 0, stream, a);
     return hipGetLastError();
 }
@@ -985,12 +1013,16 @@ template <typename T, int D>
 static hipError_t dispatch_fwd_d(FwdArgs& a, hipStream_t s) {
     const bool rope = a.p.rope == MPATTN_ROPE_FUSED;
     const bool dense = a.p.chain_mask != nullptr;
-    if (a.p.sqrt_softmax) {
-        if (rope) return dense ? launch_fwd<T, D, true, true, true>(a, s) : launch_fwd<T, D, true, false, true>(a, s);
-        return dense ? launch_fwd<T, D, false, true, true>(a, s) : launch_fwd<T, D, false, false, true>(a, s);
+    if (a.p.sqrt_softmax) {  // (dropout with sqrt-softmax is rejected by the API)
+        if (rope) return dense ? launch_fwd<T, D, true, true, true, false>(a, s) : launch_fwd<T, D, true, false, true, false>(a, s);
+        return dense ? launch_fwd<T, D, false, true, true, false>(a, s) : launch_fwd<T, D, false, false, true, false>(a, s);
     }
-    if (rope) return dense ? launch_fwd<T, D, true, true, false>(a, s) : launch_fwd<T, D, true, false, false>(a, s);
-    return dense ? launch_fwd<T, D, false, true, false>(a, s) : launch_fwd<T, D, false, false, false>(a, s);
+    if (a.p.dropout_p > 0.f) {
+        if (rope) return dense ? launch_fwd<T, D, true, true, false, true>(a, s) : launch_fwd<T, D, true, false, false, true>(a, s);
+        return dense ? launch_fwd<T, D, false, true, false, true>(a, s) : launch_fwd<T, D, false, false, false, true>(a, s);
+    }
+    if (rope) return dense ? launch_fwd<T, D, true, true, false, false>(a, s) : launch_fwd<T, D, true, false, false, false>(a, s);
+    return dense ? launch_fwd<T, D, false, true, false, false>(a, s) : launch_fwd<T, D, false, false, false, false>(a, s);
 }
 
 template <typename T>
@@ -1014,6 +1046,7 @@ hipError_t launch_fwd16(const mpattn_fwd_params& p, hipStream_t stream) {
     const float f = p.scale * kLog2e * (p.sqrt_softmax ? 0.5f : 1.0f);
     a.qmul = fused ? f : 1.0f;
     a.c = fused ? 1.0f : f;
+    a.drop = drop_cfg(p.dropout_p, p.dropout_seed);
     if (p.dtype == MPATTN_BF16) return dispatch_fwd_t<bf16_t>(a, stream);
     return dispatch_fwd_t<fp16_t>(a, stream);
 }

@@ -23,20 +23,25 @@ def _check_inputs(q_self, k_self, v_self, q_multi, k_multi, v_multi, chain_mask,
     return B, H, T, D
 
 
-def _resolve_dropout(dropout_p, training):
+def _resolve_dropout(dropout_p, training, dropout_seed=None):
+    """Effective (p, seed): p is 0 outside training; a missing seed is drawn
+    from torch's default CPU generator (so ``torch.manual_seed`` fixes it), as
+    the reference draws its per-call seed (multi_pathway_attention_fp16.py:187).
+    """
     p = float(dropout_p) if training else 0.0
-    if p != 0.0:
-        raise _lib.MpattnUnsupported(
-            _lib.MPATTN_ERR_UNSUPPORTED, "fused_multi_pathway_attention",
-            f"dropout_p={p}: attention dropout is not implemented (the reference "
-            "never enables it; pass training=False or dropout_p=0)")
-    return p
+    if not 0.0 <= p < 1.0:
+        raise ValueError(f"dropout_p must be in [0, 1), got {p}")
+    if p == 0.0:
+        return 0.0, 0
+    if dropout_seed is None:
+        dropout_seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
+    return p, int(dropout_seed) & 0xFFFFFFFFFFFFFFFF
 
 
 def fused_multi_pathway_attention(q_self, k_self, v_self, q_multi, k_multi, v_multi,
                                   chain_mask=None, dropout_p=0.0, training=True, qpp=None,
                                   sqrt_softmax=False, *, chain_ids=None, key_padding_mask=None,
-                                  rope=False, scale=None):
+                                  rope=False, scale=None, dropout_seed=None):
     """Multi-pathway attention, no (B, H, T, T) logits materialised.
 
     Same contract as the reference: q/k/v of both pathways are (B, H, T, D);
@@ -51,19 +56,24 @@ def fused_multi_pathway_attention(q_self, k_self, v_self, q_multi, k_multi, v_mu
                         kernel; q/k are then the raw projections.
       scale:            logit scale; default 1 (pre-scaled q) or D^-1/2 when
                         ``rope`` is set.
+      dropout_seed:     64-bit seed of the dropout mask (default: drawn from
+                        torch's CPU generator). With ``dropout_p`` > 0 in
+                        training, each element of P is dropped independently
+                        (a hash of seed, b*H+h, query, key) and the kept ones
+                        scaled by 1 / (1 - p); 16-bit inputs only.
     ``qpp`` is a Triton tuning hint and is ignored.
 
     Returns a new (B, H, T, D) tensor in the input dtype.
     """
     B, H, T, D = _check_inputs(q_self, k_self, v_self, q_multi, k_multi, v_multi,
                                chain_mask, chain_ids)
-    _resolve_dropout(dropout_p, training)
+    p, seed = _resolve_dropout(dropout_p, training, dropout_seed)
     if scale is None:
         scale = D ** -0.5 if rope else 1.0
     return _lib.mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi,
                            chain_ids=chain_ids, chain_mask=None if chain_ids is not None else chain_mask,
                            key_padding_mask=key_padding_mask, rope=rope, scale=scale,
-                           sqrt_softmax=sqrt_softmax)
+                           sqrt_softmax=sqrt_softmax, dropout_p=p, dropout_seed=seed)
 
 
 def fused_multi_pathway_attention_fp16(q_self, k_self, v_self, q_multi, k_multi, v_multi,

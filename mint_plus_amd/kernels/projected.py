@@ -30,14 +30,14 @@ def _heads(t, E, H):
 class _FromQKVFn(Function):
     @staticmethod
     def forward(ctx, qkv_self, qkv_multi, num_heads, chain_ids, chain_mask, key_padding_mask, rope,
-                scale, sqrt_softmax):
+                scale, sqrt_softmax, dropout_p, dropout_seed):
         T, B, E3 = qkv_self.shape
         E = E3 // 3
         ins = _heads(qkv_self, E, num_heads) + _heads(qkv_multi, E, num_heads)
         out = torch.empty((T, B, E), dtype=qkv_self.dtype, device=qkv_self.device)
         sel = dict(chain_ids=chain_ids, chain_mask=None if chain_ids is not None else chain_mask,
                    key_padding_mask=key_padding_mask, rope=rope, scale=scale,
-                   sqrt_softmax=sqrt_softmax)
+                   sqrt_softmax=sqrt_softmax, dropout_p=dropout_p, dropout_seed=dropout_seed)
         _, lse = _lib.mpattn_fwd(*ins, out=_heads(out, E, num_heads)[0], need_lse=True, **sel)
         ctx.save_for_backward(qkv_self, qkv_multi, out, lse)
         ctx.sel = sel
@@ -57,13 +57,13 @@ class _FromQKVFn(Function):
             _lib.mpattn_bwd(*_heads(qkv_self, E, H), *_heads(qkv_multi, E, H),
                             _heads(out, E, H)[0], lse, _heads(grad_out, E, H)[0],
                             grads=_heads(g_self, E, H) + _heads(g_multi, E, H), **ctx.sel)
-        return g_self, g_multi, None, None, None, None, None, None, None
+        return g_self, g_multi, None, None, None, None, None, None, None, None, None
 
 
 def multi_pathway_attention_from_qkv(qkv_self, qkv_multi, num_heads, chain_mask=None,
                                      dropout_p=0.0, training=True, sqrt_softmax=False, *,
                                      chain_ids=None, key_padding_mask=None, rope=True,
-                                     scale=None):
+                                     scale=None, dropout_seed=None):
     """Multi-pathway attention on the (T, B, 3E) outputs of the two fused QKV
     projections (self pathway first); returns O as (T, B, E). Differentiable
     w.r.t. both projection outputs.
@@ -72,6 +72,8 @@ def multi_pathway_attention_from_qkv(qkv_self, qkv_multi, num_heads, chain_mask=
     pathway's Q and K; ``scale`` defaults to ``head_dim ** -0.5``. Chain
     selection by ``chain_ids`` (B, T) or ``chain_mask`` (B, T, T), True =
     different chains; ``key_padding_mask`` (B, T), True = padded key.
+    ``dropout_p`` applies in training only (per-element mask from
+    ``dropout_seed``, default drawn from torch's CPU generator).
     """
     if qkv_self.dim() != 3 or qkv_self.shape != qkv_multi.shape:
         raise AssertionError("qkv_self / qkv_multi must both be (T, B, 3E)")
@@ -79,7 +81,7 @@ def multi_pathway_attention_from_qkv(qkv_self, qkv_multi, num_heads, chain_mask=
     if E3 % (3 * num_heads):
         raise AssertionError(f"3E={E3} is not divisible by 3 * num_heads={3 * num_heads}")
     D = E3 // (3 * num_heads)
-    _resolve_dropout(dropout_p, training)
+    p, seed = _resolve_dropout(dropout_p, training, dropout_seed)
     if chain_ids is None and (chain_mask is None or tuple(chain_mask.shape) != (B, T, T)):
         raise AssertionError(f"chain_ids (B, T) or chain_mask (B, T, T) = {(B, T, T)} required")
     if scale is None:
@@ -87,4 +89,4 @@ def multi_pathway_attention_from_qkv(qkv_self, qkv_multi, num_heads, chain_mask=
     qkv_self = qkv_self if qkv_self.is_contiguous() else qkv_self.contiguous()
     qkv_multi = qkv_multi if qkv_multi.is_contiguous() else qkv_multi.contiguous()
     return _FromQKVFn.apply(qkv_self, qkv_multi, int(num_heads), chain_ids, chain_mask,
-                            key_padding_mask, bool(rope), float(scale), bool(sqrt_softmax))
+                            key_padding_mask, bool(rope), float(scale), bool(sqrt_softmax), p, seed)

@@ -23,6 +23,12 @@ It restates, in float64 numpy, the math of the reference's eager path:
   ``mint_plus/models/kernels/multi_pathway_attention.py:163-167``.
 * ``sqrt_softmax``: ``O = sum_j sqrt(P_ij) V_j``
   (``multi_pathway_attention.py:138-152,164-165``).
+* Dropout: per element of P, ``keep = rand > p`` and ``P / (1 - p)``, as the
+  reference's kernels apply it (``kernels/__init__.py:118-122``,
+  ``profiles/bench_optimizations.py:798-803``), with the row sum over the
+  undropped P. The reference draws one Triton ``tl.rand`` value per program;
+  this build's mask is a counter-based hash of (seed, b*H+h, query, key)
+  (the definition in ``include/mpattn.h``), restated by ``dropout_keep``.
 
 Gradients are analytic (softmax backward ``dS = P * (dP - rowsum(P*dP))``
 and the transpose of the RoPE rotation). The reference's Triton backward
@@ -40,7 +46,13 @@ How each function is pinned (``tests/test_oracle.py``):
   reduction to plain SDPA with RoPE, invariants (chain-label permutation,
   appended padded keys, constant V, zero Q), L = 1, and a pure-Python
   triple loop on tiny inputs.
-* ``mpattn_backward``: central finite differences of ``mpattn_forward``.
+* ``mpattn_backward``: central finite differences of ``mpattn_forward``
+  (also with dropout: the mask is fixed by the seed).
+* ``fmix32``: MurmurHash3_x86_32 known answers (the finaliser is the whole
+  hash of the empty string, and inside the hash of longer ones).
+* ``dropout_keep``: p = 0 keeps everything, the kept fraction is 1 - p within
+  binomial bounds, rows / keys / heads / seeds give uncorrelated masks, and
+  a pure-Python restatement of the formula on a few elements.
 * ``combine_forward``: equals ``mpattn_forward`` when fed the logits of the
   two pathways computed by torch (bmm, scale, -inf padding); all-same-chain
   reduces to ``torch.softmax(intra) @ Vs``.
@@ -118,19 +130,67 @@ def _probs(s_self, s_multi, cross, key_pad):
     return p, lse
 
 
+def fmix32(x):
+    """MurmurHash3's 32-bit finaliser, elementwise on uint32 arrays."""
+    x = np.asarray(x, dtype=np.uint32).copy()
+    x ^= x >> np.uint32(16)
+    x *= np.uint32(0x85EBCA6B)
+    x ^= x >> np.uint32(13)
+    x *= np.uint32(0xC2B2AE35)
+    x ^= x >> np.uint32(16)
+    return x
+
+
+def dropout_threshold(p):
+    """round(p * 2^24): an element is kept when the top 24 bits of its hash
+    are >= this."""
+    return int(np.floor(np.float64(np.float32(p)) * 16777216.0 + 0.5))
+
+
+def dropout_keep(B, H, L, p, seed):
+    """(B, H, L, L) bool keep mask of attention dropout (the definition in
+    ``include/mpattn.h``): element (b, h, i, j) is kept when
+    ``fmix32(row ^ (j * 0x85EBCA77 + hi)) >> 8 >= round(p * 2^24)`` with
+    ``row = fmix32(lo ^ (b*H + h) * 0xC2B2AE3D ^ i * 0x9E3779B1)``, lo / hi
+    the low / high 32 bits of ``seed``; all arithmetic modulo 2^32."""
+    seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+    lo, hi = np.uint32(seed & 0xFFFFFFFF), np.uint32(seed >> 32)
+    with np.errstate(over="ignore"):
+        bh = np.arange(B * H, dtype=np.uint32)[:, None]
+        i = np.arange(L, dtype=np.uint32)[None, :]
+        row = fmix32(lo ^ (bh * np.uint32(0xC2B2AE3D)) ^ (i * np.uint32(0x9E3779B1)))  # (BH, L)
+        col = np.arange(L, dtype=np.uint32) * np.uint32(0x85EBCA77) + hi               # (L,)
+        r = fmix32(row[:, :, None] ^ col[None, None, :])
+    keep = (r >> np.uint32(8)) >= np.uint32(dropout_threshold(p))
+    return keep.reshape(B, H, L, L)
+
+
+def _dropout_factor(shape, dropout_p, dropout_seed):
+    """Z / (1 - p) as float64 (B, H, L, L), or None without dropout."""
+    if not dropout_p:
+        return None
+    B, H, L = shape[0], shape[1], shape[2]
+    return dropout_keep(B, H, L, dropout_p, dropout_seed) / (1.0 - np.float64(np.float32(dropout_p)))
+
+
 def mpattn_forward(qs, ks, vs, qm, km, vm, chain_ids=None, chain_mask=None, key_pad=None,
-                   rope=False, scale=1.0, sqrt_softmax=False):
+                   rope=False, scale=1.0, sqrt_softmax=False, dropout_p=0.0, dropout_seed=0):
     """Multi-pathway attention forward in float64.
 
     Inputs (B, H, L, D); ``chain_ids`` (B, L) or ``chain_mask`` (B, L, L)
     (True = different chains); ``key_pad`` (B, L) bool (True = padded key).
     ``rope`` applies RoPE to q_self/k_self; ``scale`` multiplies both logits.
+    ``dropout_p`` > 0 multiplies P by ``dropout_keep(...) / (1 - p)`` after
+    the softmax (the LSE stays that of the undropped softmax).
     Returns ``(out (B,H,L,D), lse (B,H,L))``; lse is in natural-log units.
     """
     cross = cross_mask(chain_ids, chain_mask)
     _, _, s_self, s_multi, _, _ = _prepare(qs, ks, qm, km, rope, scale)
     p, lse = _probs(s_self, s_multi, cross, key_pad)
     w = np.sqrt(p) if sqrt_softmax else p
+    z = _dropout_factor(np.shape(qs), dropout_p, dropout_seed)
+    if z is not None:
+        w = w * z
     c = cross[:, None]
     vs, vm = np.asarray(vs, np.float64), np.asarray(vm, np.float64)
     out = np.einsum("bhij,bhjd->bhid", np.where(c, 0.0, w), vs) + \
@@ -139,7 +199,8 @@ def mpattn_forward(qs, ks, vs, qm, km, vm, chain_ids=None, chain_mask=None, key_
 
 
 def mpattn_backward(qs, ks, vs, qm, km, vm, grad_out, chain_ids=None, chain_mask=None,
-                    key_pad=None, rope=False, scale=1.0, sqrt_softmax=False):
+                    key_pad=None, rope=False, scale=1.0, sqrt_softmax=False, dropout_p=0.0,
+                    dropout_seed=0):
     """Gradients (dq_s, dk_s, dv_s, dq_m, dk_m, dv_m) of
     ``sum(grad_out * mpattn_forward(...)[0])`` in float64."""
     cross = cross_mask(chain_ids, chain_mask)
@@ -150,11 +211,15 @@ def mpattn_backward(qs, ks, vs, qm, km, vm, grad_out, chain_ids=None, chain_mask
     p, _ = _probs(s_self, s_multi, cross, key_pad)
     c = cross[:, None]
     w = np.sqrt(p) if sqrt_softmax else p
-    w_s, w_m = np.where(c, 0.0, w), np.where(c, w, 0.0)
+    z = _dropout_factor(np.shape(qs), dropout_p, dropout_seed)
+    wz = w if z is None else w * z  # the weights that multiply V
+    w_s, w_m = np.where(c, 0.0, wz), np.where(c, wz, 0.0)
     dv_s = np.einsum("bhij,bhid->bhjd", w_s, g)
     dv_m = np.einsum("bhij,bhid->bhjd", w_m, g)
-    # dW_ij = dO_i . V_sel(ij), j
+    # dW_ij = dO_i . V_sel(ij), j, through the dropout factor
     dw = np.where(c, np.einsum("bhid,bhjd->bhij", g, vm), np.einsum("bhid,bhjd->bhij", g, vs))
+    if z is not None:
+        dw = dw * z
     if sqrt_softmax:
         # W = sqrt(P): P * dP = W * dW / 2
         pdp = 0.5 * w * dw

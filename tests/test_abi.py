@@ -37,7 +37,7 @@ def test_exports_every_header_function(lib):
 
 
 def test_version_and_strings(lib):
-    assert lib.mpattn_version() == 2
+    assert lib.mpattn_version() == 3
     assert lib.mpattn_strerror(0) == b"success"
     assert lib.mpattn_strerror(-2) == b"unsupported configuration"
     assert lib.mpattn_strerror(-99) == b"unknown error"
@@ -54,6 +54,44 @@ def test_struct_layout_matches_header():
     b = _lib.BwdParams
     assert b.grad_out.offset == 7 * 32 and b.lse.offset == 8 * 32
     assert b.dv_multi.offset == 8 * 32 + 8 + 5 * 32
+
+
+_STRUCTS = {
+    "mpattn_fwd_params": _lib.FwdParams,
+    "mpattn_bwd_params": _lib.BwdParams,
+    "mpattn_combine_fwd_params": _lib.CombineFwdParams,
+    "mpattn_combine_bwd_params": _lib.CombineBwdParams,
+}
+
+
+def test_struct_offsets_match_c_compiler(tmp_path):
+    """Every field's offset and every struct's size, as the C compiler lays
+    out include/mpattn.h, equals the ctypes mirror's."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "mpattn.h"', "int main(void) {"]
+    for cname, cls in _STRUCTS.items():
+        lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    inc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+    subprocess.run([cc, "-std=c99", "-I", inc, str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    got = {}
+    for line in out.splitlines():
+        cname, field, val = line.split()
+        got[(cname, field)] = int(val)
+    for cname, cls in _STRUCTS.items():
+        assert got[(cname, "sizeof")] == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert got[(cname, fname)] == getattr(cls, fname).offset, (cname, fname)
 
 
 def test_workspace_sizes(lib):
@@ -96,7 +134,11 @@ FWD_CASES = [
     (dict(chain_mask=1 << 23), _lib.MPATTN_ERR_INVALID, "exactly one"),
     (dict(chain_id=None), _lib.MPATTN_ERR_INVALID, "exactly one"),
     (dict(rope_cos=None), _lib.MPATTN_ERR_INVALID, "rope tables"),
-    (dict(dropout_p=0.1), _lib.MPATTN_ERR_UNSUPPORTED, "dropout"),
+    (dict(dropout_p=-0.1), _lib.MPATTN_ERR_INVALID, "dropout"),
+    (dict(dropout_p=1.0), _lib.MPATTN_ERR_INVALID, "dropout"),
+    (dict(dropout_p=float("nan")), _lib.MPATTN_ERR_INVALID, "dropout"),
+    (dict(dropout_p=0.1, dtype=_lib.MPATTN_FP32), _lib.MPATTN_ERR_UNSUPPORTED, "dropout"),
+    (dict(dropout_p=0.1, sqrt_softmax=1), _lib.MPATTN_ERR_UNSUPPORTED, "dropout"),
     (dict(q_self=_lib.Tensor4(None, 0, 0, 32)), _lib.MPATTN_ERR_INVALID, "null"),
     (dict(k_self=_lib.Tensor4((1 << 20) + 8, 40960, 2048, 32)), _lib.MPATTN_ERR_UNSUPPORTED, "aligned"),
     (dict(v_multi=_lib.Tensor4(1 << 20, 40960, 2048, 36)), _lib.MPATTN_ERR_UNSUPPORTED, "multiples"),
@@ -233,3 +275,22 @@ def test_combine_python_rejects_non_bool_mask():
     lg = torch.zeros(1, 2, 16, 16)
     with pytest.raises(AssertionError):
         m.fused_multimer_combine(lg, lg, torch.zeros(1, 16, 16, dtype=torch.int32), x, x)
+
+
+def test_resolve_dropout():
+    """Dropout arguments: off outside training, p in [0, 1), the seed drawn
+    from torch's CPU generator when not given."""
+    from mint_plus_amd.kernels.multi_pathway_attention import _resolve_dropout
+    assert _resolve_dropout(0.5, False) == (0.0, 0)
+    assert _resolve_dropout(0.0, True) == (0.0, 0)
+    assert _resolve_dropout(0.25, True, 7) == (0.25, 7)
+    assert _resolve_dropout(0.25, True, -1) == (0.25, (1 << 64) - 1)
+    for bad in (-0.1, 1.0, 1.5, float("nan")):
+        with pytest.raises(ValueError):
+            _resolve_dropout(bad, True)
+    torch.manual_seed(3)
+    a = _resolve_dropout(0.1, True)
+    torch.manual_seed(3)
+    b = _resolve_dropout(0.1, True)
+    c = _resolve_dropout(0.1, True)
+    assert a == b and a != c

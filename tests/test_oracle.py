@@ -216,6 +216,101 @@ def test_forward_sqrt_softmax_closed_form():
 
 
 # ---------------------------------------------------------------------------
+# Dropout mask
+# ---------------------------------------------------------------------------
+def _murmur3_x86_32(data, seed):
+    """MurmurHash3_x86_32 (Appleby's published algorithm), body in Python
+    ints, finalised by the oracle's fmix32."""
+    c1, c2, m32 = 0xCC9E2D51, 0x1B873593, 0xFFFFFFFF
+    rotl = lambda x, r: ((x << r) | (x >> (32 - r))) & m32
+    h, n = seed, len(data)
+    for i in range(0, n // 4 * 4, 4):
+        k = int.from_bytes(data[i:i + 4], "little")
+        k = (rotl((k * c1) & m32, 15) * c2) & m32
+        h = (rotl(h ^ k, 13) * 5 + 0xE6546B64) & m32
+    tail = data[n // 4 * 4:]
+    if tail:
+        k = int.from_bytes(tail, "little")
+        h ^= (rotl((k * c1) & m32, 15) * c2) & m32
+    return int(orc.fmix32(np.uint32(h ^ n)))
+
+
+def test_fmix32_murmur3_known_answers():
+    """Published MurmurHash3_x86_32 test vectors; for the empty string the
+    hash is fmix32(seed)."""
+    assert int(orc.fmix32(np.uint32(0))) == 0
+    assert int(orc.fmix32(np.uint32(1))) == 0x514E28B7
+    assert int(orc.fmix32(np.uint32(0xFFFFFFFF))) == 0x81F16F39
+    assert _murmur3_x86_32(b"test", 0) == 0xBA6BD213
+    assert _murmur3_x86_32(b"Hello, world!", 1234) == 0xFAF6CDB3
+    # vectorised form == scalar form
+    xs = np.array([0, 1, 0xFFFFFFFF, 12345, 0x80000000], dtype=np.uint32)
+    assert [int(v) for v in orc.fmix32(xs)] == [int(orc.fmix32(np.uint32(v))) for v in xs]
+
+
+def test_dropout_keep_scalar_restatement():
+    """A few elements against the formula evaluated with Python ints: a
+    transposed (i, j), a wrong head index or a swapped seed word fails."""
+    B, H, L, p, seed = 2, 3, 40, 0.3, 0x1234_5678_9ABC_DEF0
+    keep = orc.dropout_keep(B, H, L, p, seed)
+    lo, hi, m32 = seed & 0xFFFFFFFF, seed >> 32, 0xFFFFFFFF
+    f = lambda x: int(orc.fmix32(np.uint32(x & m32)))
+    thr = int(p * 2**24 + 0.5)
+    for b, h, i, j in [(0, 0, 0, 0), (1, 2, 39, 0), (0, 1, 3, 17), (1, 0, 20, 39), (1, 2, 7, 8)]:
+        row = f(lo ^ ((b * H + h) * 0xC2B2AE3D) ^ (i * 0x9E3779B1))
+        r = f(row ^ ((j * 0x85EBCA77 + hi) & m32))
+        assert bool(keep[b, h, i, j]) == ((r >> 8) >= thr), (b, h, i, j)
+    # asymmetric in (i, j), and the head index matters
+    assert not np.array_equal(keep[0, 0], keep[0, 0].T)
+    assert not np.array_equal(keep[0, 0], keep[0, 1])
+
+
+def test_dropout_keep_statistics():
+    B, H, L = 2, 3, 256
+    n = B * H * L * L
+    assert orc.dropout_keep(B, H, L, 0.0, 5).all()  # p = 0 keeps everything
+    for p in (0.1, 0.5, 0.9):
+        k = orc.dropout_keep(B, H, L, p, 77)
+        sd = np.sqrt(p * (1 - p) / n)
+        assert abs(k.mean() - (1 - p)) < 6 * sd, (p, k.mean())
+        # neighbouring keys / queries and different heads are independent
+        q = (1 - p) ** 2
+        sd2 = np.sqrt(q * (1 - q) / n) * 2
+        assert abs((k[..., 1:] & k[..., :-1]).mean() - q) < 6 * sd2
+        assert abs((k[:, :, 1:] & k[:, :, :-1]).mean() - q) < 6 * sd2
+        assert abs((k[:, 1:] & k[:, :-1]).mean() - q) < 6 * sd2
+    # the seed (both words) changes the mask, independently
+    a = orc.dropout_keep(1, 2, 128, 0.5, 1)
+    for other in (2, 1 + (1 << 32)):
+        b = orc.dropout_keep(1, 2, 128, 0.5, other)
+        assert abs((a == b).mean() - 0.5) < 0.02
+
+
+def test_forward_dropout_vs_torch_expression():
+    """O = (softmax * Z / (1 - p)) split by pathway, with the softmax from
+    torch over the concatenated-feature logits; LSE unchanged by dropout."""
+    rng = np.random.default_rng(11)
+    B, H, L, D, p = 2, 2, 33, 16, 0.25
+    xs = rand_inputs(rng, B, H, L, D)
+    cid = two_chain_ids(rng, B, L)
+    kp = tail_padding(rng, B, L, 0.2)
+    out, lse = orc.mpattn_forward(*xs, chain_ids=cid, key_pad=kp, rope=True, scale=0.3,
+                                  dropout_p=p, dropout_seed=99)
+    _, lse0 = orc.mpattn_forward(*xs, chain_ids=cid, key_pad=kp, rope=True, scale=0.3)
+    np.testing.assert_array_equal(lse, lse0)
+    _, logits, _ = sdpa_concat(*xs, cid, kp, True, 0.3)
+    lg = logits.masked_fill(torch.as_tensor(kp)[:, None, None, :], float("-inf"))
+    P = torch.softmax(lg, dim=-1)
+    P = torch.nan_to_num(P, nan=0.0)
+    Z = torch.as_tensor(orc.dropout_keep(B, H, L, p, 99)).double() / (1 - np.float32(p))
+    same = torch.as_tensor(cid[:, :, None] == cid[:, None, :])[:, None]
+    Pd = P * Z
+    ref = torch.where(same, Pd, 0) @ torch.as_tensor(xs[2]) + \
+        torch.where(same, 0, Pd) @ torch.as_tensor(xs[5])
+    np.testing.assert_allclose(out, ref.numpy(), atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
 # Backward
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("rope", [False, True])
@@ -233,8 +328,9 @@ def test_backward_vs_autograd_of_sdpa_concat(rope):
         np.testing.assert_allclose(g, leaf.grad.numpy(), atol=1e-11)
 
 
-@pytest.mark.parametrize("sqrt_softmax", [False, True])
-def test_backward_finite_differences(sqrt_softmax):
+@pytest.mark.parametrize("sqrt_softmax,dropout_p", [(False, 0.0), (True, 0.0), (False, 0.3)])
+def test_backward_finite_differences(sqrt_softmax, dropout_p):
+    """Central differences; with dropout the mask is fixed by the seed."""
     rng = np.random.default_rng(30 + sqrt_softmax)
     B, H, L, D = 1, 2, 14, 8
     xs = rand_inputs(rng, B, H, L, D, sigma=0.7)
@@ -242,7 +338,8 @@ def test_backward_finite_differences(sqrt_softmax):
     kp = np.zeros((B, L), bool)
     kp[0, -3:] = True
     go = rng.standard_normal((B, H, L, D))
-    kw = dict(chain_ids=cid, key_pad=kp, rope=True, scale=0.35, sqrt_softmax=sqrt_softmax)
+    kw = dict(chain_ids=cid, key_pad=kp, rope=True, scale=0.35, sqrt_softmax=sqrt_softmax,
+              dropout_p=dropout_p, dropout_seed=4242)
     grads = orc.mpattn_backward(*xs, go, **kw)
 
     def f(args):
