@@ -159,7 +159,8 @@ typedef struct mpattn_combine_fwd_params {
     int64_t mask_stride_b, mask_stride_q, mask_stride_k;
     int32_t B, H, L, D;
     int32_t dtype;
-    float dropout_p;         /* must be 0                                    */
+    float dropout_p;         /* attention dropout in [0, 1)                  */
+    uint64_t dropout_seed;   /* the mask of mpattn_fwd's dropout definition */
 } mpattn_combine_fwd_params;
 
 typedef struct mpattn_combine_bwd_params {
@@ -173,7 +174,8 @@ typedef struct mpattn_combine_bwd_params {
                                 256-byte aligned                            */
     int32_t B, H, L, D;
     int32_t dtype;
-    float dropout_p;         /* must be 0                                    */
+    float dropout_p;         /* the forward's dropout_p and dropout_seed    */
+    uint64_t dropout_seed;
 } mpattn_combine_bwd_params;
 
 /* Forward of the combine: O = softmax(where(mask, inter, intra)) split by

@@ -97,7 +97,7 @@ class CombineFwdParams(ctypes.Structure):
         ("mask_stride_k", ctypes.c_int64),
         ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("L", ctypes.c_int32), ("D", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
-        ("dropout_p", ctypes.c_float),
+        ("dropout_p", ctypes.c_float), ("dropout_seed", ctypes.c_uint64),
     ]
 
 
@@ -114,7 +114,7 @@ class CombineBwdParams(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("L", ctypes.c_int32), ("D", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
-        ("dropout_p", ctypes.c_float),
+        ("dropout_p", ctypes.c_float), ("dropout_seed", ctypes.c_uint64),
     ]
 
 
@@ -412,9 +412,10 @@ def _combine_common(intra_logits, inter_logits, chain_mask, intra_values, inter_
 
 
 def mpattn_combine_fwd(intra_logits, inter_logits, chain_mask, intra_values, inter_values, *,
-                       dropout_p=0.0, need_lse=False):
+                       dropout_p=0.0, dropout_seed=0, need_lse=False):
     """Launch the materialised-logit combine; returns ``out`` (B, H, L, D)
-    (and the fp32 (B, H, L) log-sum-exp when ``need_lse``)."""
+    (and the fp32 (B, H, L) log-sum-exp when ``need_lse``). Dropout uses the
+    fused op's mask definition for ``dropout_seed``."""
     B, H, L, D, cm = _combine_common(intra_logits, inter_logits, chain_mask, intra_values,
                                      inter_values)
     dev = intra_values.device
@@ -432,6 +433,7 @@ def mpattn_combine_fwd(intra_logits, inter_logits, chain_mask, intra_values, int
     p.B, p.H, p.L, p.D = B, H, L, D
     p.dtype = _DTYPES[vs.dtype]
     p.dropout_p = float(dropout_p)
+    p.dropout_seed = int(dropout_seed) & 0xFFFFFFFFFFFFFFFF
     rc = load_library().mpattn_combine_fwd(ctypes.byref(p), _stream_handle(dev))
     _check(rc, "mpattn_combine_fwd")
     del il, el, vs, vm, cm
@@ -439,7 +441,7 @@ def mpattn_combine_fwd(intra_logits, inter_logits, chain_mask, intra_values, int
 
 
 def mpattn_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values, inter_values,
-                       grad_out, *, dropout_p=0.0):
+                       grad_out, *, dropout_p=0.0, dropout_seed=0):
     """Launch the combine backward; returns (d_intra_logits, d_inter_logits,
     d_intra_values, d_inter_values) in the inputs' dtype."""
     B, H, L, D, cm = _combine_common(intra_logits, inter_logits, chain_mask, intra_values,
@@ -470,6 +472,7 @@ def mpattn_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values, int
     p.B, p.H, p.L, p.D = B, H, L, D
     p.dtype = _DTYPES[vs.dtype]
     p.dropout_p = float(dropout_p)
+    p.dropout_seed = int(dropout_seed) & 0xFFFFFFFFFFFFFFFF
     rc = lib.mpattn_combine_bwd(ctypes.byref(p), _stream_handle(dev))
     _check(rc, "mpattn_combine_bwd")
     del il, el, vs, vm, go, cm, ws

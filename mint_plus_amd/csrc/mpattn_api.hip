@@ -98,8 +98,8 @@ int check_combine(int B, int H, int L, int D, int dtype, const uint8_t* mask, in
         return fail(MPATTN_ERR_UNSUPPORTED, "combine: head dim %d not supported (multiple of 8, <= 64)", D);
     if (!mask) return fail(MPATTN_ERR_INVALID, "chain_mask required");
     if (msb < 0 || msq < 0 || msk < 0) return fail(MPATTN_ERR_UNSUPPORTED, "chain_mask: negative stride");
-    if (dropout_p != 0.f)
-        return fail(MPATTN_ERR_UNSUPPORTED, "dropout_p must be 0 (got %g)", (double)dropout_p);
+    if (!(dropout_p >= 0.f && dropout_p < 1.f))
+        return fail(MPATTN_ERR_INVALID, "dropout_p must be in [0, 1) (got %g)", (double)dropout_p);
     const int64_t nblk = (int64_t)B * H * ((L + 63) / 64);
     if (nblk > 0x7fffffffLL) return fail(MPATTN_ERR_UNSUPPORTED, "problem too large for one launch");
     return MPATTN_OK;

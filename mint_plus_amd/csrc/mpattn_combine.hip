@@ -12,7 +12,9 @@
 //
 // Backward: dS_ij = P_ij (dO_i . Vsel_j - Delta_i), Delta_i = dO_i . O_i,
 // split into d_intra / d_inter by the mask; dVs_j = sum_i P_ij [!mask] dO_i,
-// dVm_j likewise.
+// dVm_j likewise. With dropout (keep mask Z of the fused op's definition,
+// r = 1 / (1 - p)): O uses r Z P, dVs / dVm use r Z P, and dO_i . Vsel_j is
+// replaced by r Z_ij dO_i . Vsel_j; the softmax and its LSE are undropped.
 //
 // The op streams 2 L^2 logits per (b, h) against O(L D) other data, so it is
 // HBM-bound; the kernels read every logit once per pass with 16-byte loads
@@ -55,6 +57,8 @@ struct CombineArgs {
     int64_t dvs_sb, dvs_sh, dvs_st, dvm_sb, dvm_sh, dvm_st;
     float *lse, *delta;               // (B*H*L)
     int B, H, L, D;
+    DropCfg drop;
+    int drop_on;                      // dropout_p > 0
 };
 
 constexpr float kLog2eC = 1.4426950408889634f;
@@ -198,6 +202,8 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(CombineArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[n][i] = 0.f;
     float mref = -INFINITY, lsum = 0.f;
+    const bool dropon = a.drop_on != 0;
+    const uint32_t drow = dropon ? drop_row(a.drop.lo, (uint32_t)bh, (uint32_t)q) : 0u;
 
     const int nch = D / 8;  // 8-element chunks per value row
     for (int kc = 0; kc < L; kc += KC) {
@@ -259,8 +265,9 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(CombineArgs a) {
             float pi[8], pe[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float p = fast_exp2(s[j] - mu);
-                lsum += p;
+                float p = fast_exp2(s[j] - mu);
+                lsum += p;  // the row sum is over the undropped P
+                if (dropon && !drop_keep(drow, a.drop.hi, (uint32_t)(k + j), a.drop.thr)) p = 0.f;
                 const bool x = (bits >> j) & 1;
                 pi[j] = x ? 0.f : p;
                 pe[j] = x ? p : 0.f;
@@ -293,7 +300,7 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(CombineArgs a) {
     }
 
     const float lt = lsum + __shfl_xor(lsum, 32);
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    const float inv = lt > 0.f ? (dropon ? a.drop.rkeep : 1.f) / lt : 0.f;
     const int64_t row = (int64_t)bh * L + qc;
     if (a.lse && q < L && half == 0) {
         const float mu = (mref == -INFINITY) ? 0.f : mref;
@@ -426,11 +433,12 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(CombineArgs a) {
         for (int i = 0; i < 16; ++i) acc[n][i] = 0.f;
 
     const int nch = D / 8;
+    const bool dropon = a.drop_on != 0;
     for (int q0 = 0; q0 < L; q0 += 32) {
         const int qq = q0 + tq;
         const int qc = min(qq, L - 1);
         float p[8];
-        unsigned bits;
+        unsigned bits, keep = 0xFFu;  // keep: dropout bits of the 8 keys
         float dq;
         __syncthreads();
         {
@@ -442,17 +450,25 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(CombineArgs a) {
             dq = dlt[qc];
             const bool ok = qq < L && l > -INFINITY;
             const float l2 = ok ? l * kLog2eC : 0.f;
+            if (dropon) {
+                const uint32_t drow = drop_row(a.drop.lo, (uint32_t)bh, (uint32_t)qq);
+                keep = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    keep |= (unsigned)drop_keep(drow, a.drop.hi, (uint32_t)(k8 + j), a.drop.thr) << j;
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const bool x = (bits >> j) & 1;
                 p[j] = ok ? fast_exp2((x ? se[j] : si[j]) * kLog2eC - l2) : 0.f;
+                const float pz = (keep >> j) & 1 ? p[j] : 0.f;  // the dV operand: Z P
                 if constexpr (F32) {
                     float* P = (float*)lp;
-                    P[tq * PF_RS + tg * 8 + j] = x ? 0.f : p[j];
-                    P[32 * PF_RS + tq * PF_RS + tg * 8 + j] = x ? p[j] : 0.f;
+                    P[tq * PF_RS + tg * 8 + j] = x ? 0.f : pz;
+                    P[32 * PF_RS + tq * PF_RS + tg * 8 + j] = x ? pz : 0.f;
                 } else {
-                    lp[(tg * 8 + j) * PT_RS + tq] = (T)(x ? 0.f : p[j]);
-                    lp[64 * PT_RS + (tg * 8 + j) * PT_RS + tq] = (T)(x ? p[j] : 0.f);
+                    lp[(tg * 8 + j) * PT_RS + tq] = (T)(x ? 0.f : pz);
+                    lp[64 * PT_RS + (tg * 8 + j) * PT_RS + tq] = (T)(x ? pz : 0.f);
                 }
             }
         }
@@ -534,7 +550,9 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(CombineArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const bool x = (bits >> j) & 1;
-                const float ds = p[j] * ((x ? wm[j] : ws[j]) - dq);
+                float w = x ? wm[j] : ws[j];
+                if (dropon) w = (keep >> j) & 1 ? w * a.drop.rkeep : 0.f;
+                const float ds = p[j] * (w - dq);
                 di[j] = x ? 0.f : ds;
                 de[j] = x ? ds : 0.f;
             }
@@ -566,7 +584,7 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(CombineArgs a) {
                 if (d < D) {
                     float v[4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) v[r] = acc[n][gi * 4 + r];
+                    for (int r = 0; r < 4; ++r) v[r] = acc[n][gi * 4 + r] * (dropon ? a.drop.rkeep : 1.f);
                     store4<T>(dv, d, v);
                 }
             }
@@ -632,6 +650,8 @@ hipError_t launch_combine_fwd(const mpattn_combine_fwd_params& p, float* lse_buf
                 p.mask_stride_b, p.mask_stride_q, p.mask_stride_k, p.B, p.H, p.L, p.D);
     a.out = (void*)p.out.ptr; a.o_sb = p.out.stride_b; a.o_sh = p.out.stride_h; a.o_st = p.out.stride_t;
     a.lse = lse_buf;
+    a.drop = drop_cfg(p.dropout_p, p.dropout_seed);
+    a.drop_on = p.dropout_p > 0.f;
     const int es = p.dtype == MPATTN_FP32 ? 4 : 2;
     const bool vec = vec_ok(a, es);
     switch (p.dtype) {
@@ -655,6 +675,8 @@ hipError_t launch_combine_bwd(const mpattn_combine_bwd_params& p, hipStream_t st
     a.dvs_sh = p.d_intra_values.stride_h; a.dvs_st = p.d_intra_values.stride_t;
     a.dvm = (void*)p.d_inter_values.ptr; a.dvm_sb = p.d_inter_values.stride_b;
     a.dvm_sh = p.d_inter_values.stride_h; a.dvm_st = p.d_inter_values.stride_t;
+    a.drop = drop_cfg(p.dropout_p, p.dropout_seed);
+    a.drop_on = p.dropout_p > 0.f;
     char* ws = (char*)p.workspace;
     a.lse = (float*)ws;
     a.delta = (float*)(ws + combine_ws_offset_delta(p.B, p.H, p.L));

@@ -12,6 +12,7 @@ import torch
 from torch.autograd import Function
 
 from .. import _lib
+from .multi_pathway_attention import _resolve_dropout
 
 
 def _check_mask(chain_mask):
@@ -20,45 +21,54 @@ def _check_mask(chain_mask):
 
 
 def fused_multimer_combine(intra_logits, inter_logits, chain_mask, intra_values, inter_values,
-                           dropout_p=0.0):
+                           dropout_p=0.0, *, dropout_seed=None):
     """(B, H, T, D) combined output, ready for ``out_proj``
-    (kernels/__init__.py:179-242). ``dropout_p`` must be 0."""
+    (kernels/__init__.py:179-242). With ``dropout_p`` > 0 each element of P
+    is dropped by the fused op's hash mask for ``dropout_seed`` (default:
+    drawn from torch's CPU generator, as the reference draws its seed,
+    kernels/__init__.py:211) and the kept ones scaled by 1 / (1 - p)."""
     _check_mask(chain_mask)
+    p, seed = _resolve_dropout(dropout_p, True, dropout_seed)
     return _lib.mpattn_combine_fwd(intra_logits, inter_logits, chain_mask, intra_values,
-                                   inter_values, dropout_p=dropout_p)
+                                   inter_values, dropout_p=p, dropout_seed=seed)
 
 
 def fused_multimer_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values,
-                               inter_values, grad_output, dropout_p=0.0):
+                               inter_values, grad_output, dropout_p=0.0, *, dropout_seed=0):
     """(d_intra_logits, d_inter_logits, d_intra_values, d_inter_values) of the
-    combine (kernels/__init__.py:247-286), in the inputs' dtype."""
+    combine (kernels/__init__.py:247-286), in the inputs' dtype; with dropout,
+    ``dropout_seed`` must be the forward's."""
     _check_mask(chain_mask)
     return _lib.mpattn_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values,
-                                   inter_values, grad_output, dropout_p=dropout_p)
+                                   inter_values, grad_output, dropout_p=dropout_p,
+                                   dropout_seed=dropout_seed)
 
 
 class _MultimerCombineFn(Function):
     @staticmethod
     def forward(ctx, intra_logits, inter_logits, chain_mask, intra_values, inter_values,
-                dropout_p):
+                dropout_p, dropout_seed):
         ctx.save_for_backward(intra_logits, inter_logits, chain_mask, intra_values, inter_values)
-        ctx.dropout_p = dropout_p
+        ctx.dropout_p, ctx.dropout_seed = dropout_p, dropout_seed
         return fused_multimer_combine(intra_logits, inter_logits, chain_mask, intra_values,
-                                      inter_values, dropout_p=dropout_p)
+                                      inter_values, dropout_p=dropout_p, dropout_seed=dropout_seed)
 
     @staticmethod
     def backward(ctx, grad_output):
         il, el, cm, vs, vm = ctx.saved_tensors
         with torch.no_grad():
             d_il, d_el, d_vs, d_vm = fused_multimer_combine_bwd(
-                il, el, cm, vs, vm, grad_output.contiguous(), dropout_p=ctx.dropout_p)
-        return d_il, d_el, None, d_vs, d_vm, None
+                il, el, cm, vs, vm, grad_output.contiguous(), dropout_p=ctx.dropout_p,
+                dropout_seed=ctx.dropout_seed)
+        return d_il, d_el, None, d_vs, d_vm, None, None
 
 
 def differentiable_multimer_combine(intra_logits, inter_logits, chain_mask, intra_values,
-                                    inter_values, dropout_p=0.0):
+                                    inter_values, dropout_p=0.0, *, dropout_seed=None):
     """``fused_multimer_combine`` with autograd
-    (differentiable_attention.py:127-140)."""
+    (differentiable_attention.py:127-140); the backward reuses the forward's
+    dropout seed."""
     _check_mask(chain_mask)
+    p, seed = _resolve_dropout(dropout_p, True, dropout_seed)
     return _MultimerCombineFn.apply(intra_logits, inter_logits, chain_mask, intra_values,
-                                    inter_values, float(dropout_p))
+                                    inter_values, p, seed)

@@ -237,16 +237,21 @@ def mpattn_backward(qs, ks, vs, qm, km, vm, grad_out, chain_ids=None, chain_mask
     return dq_s, dk_s, dv_s, dq_m, dk_m, dv_m
 
 
-def combine_forward(intra_logits, inter_logits, chain_mask, vs, vm):
+def combine_forward(intra_logits, inter_logits, chain_mask, vs, vm, dropout_p=0.0,
+                    dropout_seed=0):
     """Materialised-logit combine in float64: ``where(chain_mask, inter,
     intra)`` -> one softmax over keys -> split by pathway -> ``P_intra @ Vs +
     P_inter @ Vm`` (the contract of ``fused_multimer_combine``,
     ``mint_plus/models/kernels/__init__.py:93-176``, and of the eager
     ``modules_plus.py:178-194``). Logits already carry the scale and -inf at
-    padded keys; an all -inf row gives 0. Returns ``(out, lse)``."""
+    padded keys; an all -inf row gives 0. Dropout as in ``mpattn_forward``.
+    Returns ``(out, lse)``."""
     cross = np.asarray(chain_mask, dtype=bool)
     il, el = np.asarray(intra_logits, np.float64), np.asarray(inter_logits, np.float64)
     p, lse = _probs(il, el, cross, None)
+    z = _dropout_factor(np.shape(il), dropout_p, dropout_seed)
+    if z is not None:
+        p = p * z
     c = cross[:, None]
     vs, vm = np.asarray(vs, np.float64), np.asarray(vm, np.float64)
     out = np.einsum("bhij,bhjd->bhid", np.where(c, 0.0, p), vs) + \
@@ -254,7 +259,8 @@ def combine_forward(intra_logits, inter_logits, chain_mask, vs, vm):
     return out, lse
 
 
-def combine_backward(intra_logits, inter_logits, chain_mask, vs, vm, grad_out):
+def combine_backward(intra_logits, inter_logits, chain_mask, vs, vm, grad_out, dropout_p=0.0,
+                     dropout_seed=0):
     """Gradients (d_intra_logits, d_inter_logits, d_vs, d_vm) of
     ``sum(grad_out * combine_forward(...)[0])`` in float64 (the contract of
     ``fused_multimer_combine_bwd``, ``kernels/__init__.py:247-286``)."""
@@ -264,9 +270,13 @@ def combine_backward(intra_logits, inter_logits, chain_mask, vs, vm, grad_out):
     g = np.asarray(grad_out, np.float64)
     p, _ = _probs(il, el, cross, None)
     c = cross[:, None]
-    d_vs = np.einsum("bhij,bhid->bhjd", np.where(c, 0.0, p), g)
-    d_vm = np.einsum("bhij,bhid->bhjd", np.where(c, p, 0.0), g)
+    z = _dropout_factor(np.shape(il), dropout_p, dropout_seed)
+    pz = p if z is None else p * z
+    d_vs = np.einsum("bhij,bhid->bhjd", np.where(c, 0.0, pz), g)
+    d_vm = np.einsum("bhij,bhid->bhjd", np.where(c, pz, 0.0), g)
     dw = np.where(c, np.einsum("bhid,bhjd->bhij", g, vm), np.einsum("bhid,bhjd->bhij", g, vs))
+    if z is not None:
+        dw = dw * z
     pdp = p * dw
     ds = pdp - p * pdp.sum(axis=-1, keepdims=True)
     return np.where(c, 0.0, ds), np.where(c, ds, 0.0), d_vs, d_vm

@@ -219,7 +219,8 @@ COMBINE_CASES = [
     (dict(dtype=3), _lib.MPATTN_ERR_INVALID, "dtype"),
     (dict(chain_mask=None), _lib.MPATTN_ERR_INVALID, "chain_mask"),
     (dict(mask_stride_k=-1), _lib.MPATTN_ERR_UNSUPPORTED, "negative"),
-    (dict(dropout_p=0.1), _lib.MPATTN_ERR_UNSUPPORTED, "dropout"),
+    (dict(dropout_p=1.0), _lib.MPATTN_ERR_INVALID, "dropout"),
+    (dict(dropout_p=-0.5), _lib.MPATTN_ERR_INVALID, "dropout"),
     (dict(intra_logits=_lib.Tensor4(None, 0, 0, 64)), _lib.MPATTN_ERR_INVALID, "intra_logits"),
     (dict(out=_lib.Tensor4((1 << 20) + 4, 40960, 2048, 32)), _lib.MPATTN_ERR_UNSUPPORTED, "aligned"),
 ]
@@ -249,8 +250,9 @@ def test_combine_bwd_validation(lib):
     p.workspace = (1 << 24) + 128
     assert lib.mpattn_combine_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
     p.workspace = 1 << 24
-    p.dropout_p = 0.5
-    assert lib.mpattn_combine_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_UNSUPPORTED
+    p.dropout_p = 1.5
+    assert lib.mpattn_combine_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
+    assert "dropout" in lib.mpattn_last_error().decode()
 
 
 def test_combine_workspace_size(lib):

@@ -144,3 +144,107 @@ def test_combine_150m_shape():
                                                                        vm.float())
     err = (out.float() - ref).abs()
     assert bool((err <= 2e-2 + 1e-2 * ref.abs()).all()), f"max err {err.max().item():.3g}"
+
+
+# ---------------------------------------------------------------------------
+# Dropout (the fused op's hash mask, include/mpattn.h)
+# ---------------------------------------------------------------------------
+def _code(L, D):
+    """Row j: 2^(j // D) in column j % D (see tests/test_dropout_gpu.py)."""
+    c = np.zeros((L, D))
+    j = np.arange(L)
+    c[j, j % D] = 2.0 ** (j // D)
+    return c
+
+
+@pytest.mark.parametrize("dtype,D,L", [(torch.bfloat16, 32, 128), (torch.float16, 32, 256),
+                                       (torch.float32, 32, 256), (torch.bfloat16, 16, 50)])
+def test_combine_dropout_exact_mask(dtype, D, L):
+    """Zero logits (P = 1/n over valid keys) and one-hot coded V / dO: every
+    output and dV element is an integer of keep bits times r / n, so a single
+    mask element that differs from the oracle's moves it by r / n (allowed:
+    r / (4n)). L = 50 takes the scalar-load path."""
+    print(f"[combine dropout exact] {dtype} D={D} L={L}", flush=True)
+    B, H, p, seed = 2, 3, 0.35, 0xDEADBEEF12345
+    rng = np.random.default_rng(L + D)
+    kp = tail_padding(rng, B, L, 0.15)
+    z = np.where(kp[:, None, None, :], -np.inf, np.zeros((B, H, L, L)))
+    cm = multi_chain_ids(rng, B, L, 2)
+    cm = cm[:, :, None] != cm[:, None, :]
+    code = np.broadcast_to(_code(L, D), (B, H, L, D)).copy()
+    vrand = rng.standard_normal((B, H, L, D))
+    r = lambda a: torch.from_numpy(a.astype(np.float32)).to(dtype).to(DEV)
+    cmt = torch.from_numpy(cm).to(DEV)
+    m = _m()
+    out = m.fused_multimer_combine(r(z), r(z), cmt, r(code), r(code), dropout_p=p,
+                                   dropout_seed=seed)
+    grads = m.fused_multimer_combine_bwd(r(z), r(z), cmt, r(vrand), r(vrand), r(code),
+                                         dropout_p=p, dropout_seed=seed)
+    torch.cuda.synchronize()
+    n = (~kp).sum(axis=1).astype(np.float64)
+    step = (1.0 / (1.0 - np.float64(np.float32(p))) / n)[:, None, None, None]
+    ref, _ = orc.combine_forward(z, z, cm, code, code, dropout_p=p, dropout_seed=seed)
+    err = np.abs(out.double().cpu().numpy() - ref)
+    assert (err <= 0.25 * step).all(), f"out: max err {err.max():.3g}"
+    rg = orc.combine_backward(z, z, cm, vrand.astype(np.float32).astype(np.float64),
+                              vrand.astype(np.float32).astype(np.float64), code, dropout_p=p,
+                              dropout_seed=seed)
+    for name, i in (("d_vs", 2), ("d_vm", 3)):
+        err = np.abs(grads[i].double().cpu().numpy() - rg[i])
+        assert (err <= 0.25 * step).all(), f"{name}: max err {err.max():.3g}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("L", [64, 100, 257])
+def test_combine_dropout_random(dtype, L):
+    print(f"[combine dropout random] {dtype} L={L}", flush=True)
+    D, p, seed = 32, 0.2, 99 + L
+    t, cm = make(2, 3, L, D, dtype, seed=300 + L)
+    g = [x.to(DEV) for x in t]
+    cmt = torch.from_numpy(cm).to(DEV)
+    m = _m()
+    out = m.fused_multimer_combine(g[0], g[1], cmt, g[2], g[3], dropout_p=p, dropout_seed=seed)
+    grads = m.fused_multimer_combine_bwd(g[0], g[1], cmt, g[2], g[3], g[4], dropout_p=p,
+                                         dropout_seed=seed)
+    torch.cuda.synchronize()
+    a = [x.double().numpy() for x in t]
+    ref, _ = orc.combine_forward(a[0], a[1], cm, a[2], a[3], dropout_p=p, dropout_seed=seed)
+    check(out, ref, dtype, "out")
+    rg = orc.combine_backward(*a[:2], cm, *a[2:], dropout_p=p, dropout_seed=seed)
+    fro = 1e-5 if dtype == torch.float32 else 2e-2
+    for name, x, r in zip(("d_intra_logits", "d_inter_logits", "d_vs", "d_vm"), grads, rg):
+        check(x, r, dtype, f"{name} dropout {dtype} L={L}", rel_fro=fro)
+
+
+def test_combine_dropout_autograd_seed():
+    """differentiable_multimer_combine keeps the forward's seed for the
+    backward; a fixed seed reproduces bitwise; torch.manual_seed fixes the
+    default seed."""
+    print("[combine dropout autograd]", flush=True)
+    D, L, p = 32, 96, 0.3
+    t, cm = make(1, 2, L, D, torch.bfloat16, seed=5)
+    cmt = torch.from_numpy(cm).to(DEV)
+    m = _m()
+
+    def run(**kw):
+        leaves = [x.to(DEV).requires_grad_(True) for x in t[:4]]
+        out = m.differentiable_multimer_combine(leaves[0], leaves[1], cmt, leaves[2], leaves[3],
+                                                dropout_p=p, **kw)
+        (out.float() * t[4].to(DEV).float()).sum().backward()
+        return [out.detach()] + [x.grad for x in leaves]
+
+    a = run(dropout_seed=17)
+    b = run(dropout_seed=17)
+    torch.manual_seed(3)
+    c = run()
+    torch.manual_seed(3)
+    d = run()
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    for x, y in zip(c, d):
+        assert torch.equal(x, y)
+    x = [v.double().numpy() for v in t]
+    rg = orc.combine_backward(x[0], x[1], cm, x[2], x[3], x[4], dropout_p=p, dropout_seed=17)
+    for name, g, r in zip(("d_intra_logits", "d_inter_logits", "d_vs", "d_vm"), a[1:], rg):
+        check(g, r, torch.bfloat16, f"autograd {name}", rel_fro=2e-2)

@@ -324,3 +324,41 @@ def test_dropout_long_rows():
                               scale=D ** -0.5, dropout_p=p, dropout_seed=seed)
     for name, g, r in zip(NAMES, got, ref):
         _assert16(g, r, name)
+
+
+def test_dropout_layer_fused_equals_combine_path():
+    """A multimer layer in training mode with attention dropout: the fused
+    path and the materialised combine path draw the same seed from torch's
+    CPU generator and use the same mask, so their outputs and input
+    gradients agree to the bf16 tolerance; without the same seed they do
+    not."""
+    print("[dropout layer]", flush=True)
+    from mint_plus_amd import modules as M
+    torch.manual_seed(21)
+    T, B, E, H = 160, 2, 640, 20
+    layer = M.TransformerLayer_MINT(E, 4 * E, H, use_multimer=True).to(DEV, torch.bfloat16).train()
+    layer.self_attn.dropout = 0.2
+    rng = np.random.default_rng(3)
+    x = torch.from_numpy(rng.standard_normal((T, B, E)).astype(np.float32)).to(torch.bfloat16)
+    cid = torch.from_numpy(two_chain_ids(rng, B, T)).to(DEV)
+    kp = torch.zeros(B, T, dtype=torch.bool, device=DEV)
+    kp[1, T - 12:] = True
+    go = torch.from_numpy(rng.standard_normal((T, B, E)).astype(np.float32)).to(DEV)
+
+    def run(fused, seed):
+        layer._use_fused_multi_pathway = fused
+        xi = x.to(DEV).requires_grad_(True)
+        torch.manual_seed(seed)
+        y, _ = layer(xi, self_attn_padding_mask=kp, chain_ids=cid)
+        (y.float() * go).sum().backward()
+        return y.detach().float().cpu().double().numpy(), xi.grad.float().cpu().double().numpy()
+
+    yf, gf = run(True, 100)
+    yc, gc = run(False, 100)
+    yo, _ = run(True, 101)
+    torch.cuda.synchronize()
+    valid = ~kp.cpu().numpy().T[:, :, None]  # (T, B, 1): outputs of unpadded tokens
+    _assert16(np.where(valid, yf, 0), np.where(valid, yc, 0), "layer output fused vs combine")
+    err = np.linalg.norm(gf - gc) / np.linalg.norm(gc)
+    assert err < 2e-2, f"input gradient fused vs combine: relative error {err:.3g}"
+    assert np.abs(yo - yf).max() > 0.05  # another seed, another mask

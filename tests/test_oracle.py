@@ -477,3 +477,38 @@ def test_combine_backward_finite_differences():
         fd = (f(plus) - f(minus)) / (2 * eps)
         an = float((grads[i] * d).sum())
         assert abs(fd - an) <= 1e-6 * max(1.0, abs(an)), (i, fd, an)
+
+
+def test_combine_dropout_equals_fused_op_dropout():
+    """Fed the two pathways' logits, the combine with dropout equals the fused
+    op with the same seed (forward and every gradient through the chain
+    rule of the logits), and its backward matches central differences."""
+    rng = np.random.default_rng(62)
+    B, H, L, D, p, seed = 2, 2, 20, 8, 0.3, 777
+    xs = rand_inputs(rng, B, H, L, D)
+    cid = two_chain_ids(rng, B, L)
+    kp = tail_padding(rng, B, L, 0.2)
+    il, el = _torch_logits(xs, cid, kp, 0.3)
+    cm = cid[:, :, None] != cid[:, None, :]
+    out_c, lse_c = orc.combine_forward(il, el, cm, xs[2], xs[5], dropout_p=p, dropout_seed=seed)
+    out_f, lse_f = orc.mpattn_forward(*xs, chain_ids=cid, key_pad=kp, rope=True, scale=0.3,
+                                      dropout_p=p, dropout_seed=seed)
+    np.testing.assert_allclose(out_c, out_f, atol=1e-12)
+    np.testing.assert_allclose(lse_c, lse_f, atol=1e-12)
+    go = rng.standard_normal((B, H, L, D))
+    d_il, d_el, d_vs, d_vm = orc.combine_backward(il, el, cm, xs[2], xs[5], go, dropout_p=p,
+                                                  dropout_seed=seed)
+    g = orc.mpattn_backward(*xs, go, chain_ids=cid, key_pad=kp, rope=True, scale=0.3,
+                            dropout_p=p, dropout_seed=seed)
+    np.testing.assert_allclose(d_vs, g[2], atol=1e-12)
+    np.testing.assert_allclose(d_vm, g[5], atol=1e-12)
+    # dQ_multi = scale * d_inter @ K_multi
+    np.testing.assert_allclose(0.3 * np.einsum("bhij,bhjd->bhid", d_el, xs[4]), g[3], atol=1e-12)
+    # finite differences in one logit tensor (finite entries only)
+    fin = np.isfinite(il)
+    d = np.where(fin, rng.standard_normal(il.shape), 0.0)
+    eps = 1e-6
+    f = lambda x: float((orc.combine_forward(x, el, cm, xs[2], xs[5], dropout_p=p,
+                                             dropout_seed=seed)[0] * go).sum())
+    fd = (f(np.where(fin, il + eps * d, il)) - f(np.where(fin, il - eps * d, il))) / (2 * eps)
+    assert abs(fd - float((np.where(fin, d_il, 0) * d).sum())) < 1e-6 * max(1.0, abs(fd))
