@@ -293,24 +293,28 @@ void fwd_kernel(const FwdArgs args) {
     unsigned dinc[NJ];    // bytes between stages: 64 rows (uniform)
     unsigned dlds[NJ];    // LDS offset inside a stage (uniform)
     const char* dva[NJ];  // per-lane source address of (r, c) in stage 0
-    int drw[NJ], dcol[NJ];
     int dten[NJ];         // tile index, 4 for an idle copy (uniform)
+    // (row, swizzled byte column) of copy j for lane `ln`
+    auto dma_rc = [&](int j, int ln, int& r, int& cb) {
+        const int ins0 = wave + j * W;
+        const int part = (ins0 < TOT ? ins0 : TOT - 1) % S::NI;
+        const int slot = part * 64 + ln;
+        r = slot / S::NCH;
+        cb = S::swz(r, slot % S::NCH) * 16;  // swz is an involution on the chunk index
+    };
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int ins0 = wave + j * W;
         const int ins = ins0 < TOT ? ins0 : TOT - 1;
         const int ten = ins / S::NI, part = ins % S::NI;
-        const int slot = part * 64 + lane;
-        const int r = slot / S::NCH, pc = slot % S::NCH;
-        const int cb = S::swz(r, pc) * 16;  // swz is an involution on the chunk index
+        int r, cb;
+        dma_rc(j, lane, r, cb);
         const T* tb = ten == 0 ? ks_p : ten == 1 ? km_p : ten == 2 ? vs_p : vm_p;
         const int64_t ts = ten == 0 ? ks_t : ten == 1 ? km_t : ten == 2 ? vs_t : vm_t;
         dsb[j] = (const char*)tb;
         dstr[j] = (unsigned)(ts * (int64_t)sizeof(T));
         dinc[j] = dstr[j] * kBN;
         dlds[j] = ten * S::TILE + part * 1024;
-        drw[j] = r;
-        dcol[j] = cb;
         dva[j] = dsb[j] + (r * dstr[j] + cb);
         dten[j] = ins0 < TOT ? ten : 4;
     }
@@ -330,8 +334,16 @@ void fwd_kernel(const FwdArgs args) {
 #pragma unroll
             for (int j = 0; j < NJ; ++j) va[j] = dva[j] + (unsigned)s * dinc[j];
         } else {  // last stage: clamp rows past L to L-1 (their keys are masked)
+            // The lane id comes from an opaque instruction so that (r, cb)
+            // are recomputed here instead of occupying registers all loop.
+            int ln;
+            asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) va[j] = dsb[j] + ((unsigned)min(k0 + drw[j], L - 1) * dstr[j] + dcol[j]);
+            for (int j = 0; j < NJ; ++j) {
+                int r, cb;
+                dma_rc(j, ln, r, cb);
+                va[j] = dsb[j] + ((unsigned)min(k0 + r, L - 1) * dstr[j] + cb);
+            }
         }
         const int m0v = m0_save();
         int n = 1;
@@ -921,8 +933,18 @@ void fwd_kernel(const FwdArgs args) {
             for_blocks<QB>([&](auto u_c) {
                 constexpr int u = decltype(u_c)::value;
                 if ((done >> u) & 1) return;
+                // Unrolled for chain ids and D <= 32: with an inner loop the
+                // accumulators get a second register home and every fast
+                // stage pays two copies of them. D = 64 and the dense-mask
+                // kernels keep the loop (unrolled, they spill or no longer fit
+                // their occupancy).
+                if constexpr (D == 64 || DENSE) {
 #pragma unroll 1
-                for (int st = 0; st < 2; ++st) slow_subtile(u_c, stage, cid, st, st ? c1[u] : c0[u], k0);
+                    for (int st = 0; st < 2; ++st) slow_subtile(u_c, stage, cid, st, st ? c1[u] : c0[u], k0);
+                } else {
+#pragma unroll
+                    for (int st = 0; st < 2; ++st) slow_subtile(u_c, stage, cid, st, st ? c1[u] : c0[u], k0);
+                }
             });
         }
         bf = bf + 1 == NBUF ? 0 : bf + 1;
