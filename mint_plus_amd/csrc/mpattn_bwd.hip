@@ -292,8 +292,11 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     const int ql = lane & 31, hh = lane >> 5;
     const int L = p.L, H = p.H, Lp = a.Lp;
     const int nkb = (L + 32 * W - 1) / (32 * W);
-    const int g = xcd_remap(blockIdx.x, gridDim.x);
-    const int kblk = g % nkb, bh = g / nkb;
+    // Key blocks whose keys span two chains or hold padded keys (both take
+    // the two-pathway mode for every query subtile) are dispatched first.
+    int kblk, bh;
+    dispatch_order(nkb, H, DENSE ? nullptr : reinterpret_cast<const int4*>(a.ksum), Lp / 32, (L + 31) / 32, W,
+                   true, (int64_t)3 * L * D * sizeof(T), 2 << 20, kblk, bh);
     const int b = bh / H, h = bh % H;
     const int kw0 = kblk * 32 * W + wave * 32;  // first key of this wave
     const int key = kw0 + ql;                   // this lane's key (B operand column)
@@ -629,8 +632,10 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     const int ql = lane & 31, hh = lane >> 5;
     const int L = p.L, H = p.H, Lp = a.Lp;
     const int nqb = (L + 32 * W - 1) / (32 * W);
-    const int g = xcd_remap(blockIdx.x, gridDim.x);
-    const int qblk = g % nqb, bh = g / nqb;
+    // Query blocks whose rows span two chains are dispatched first.
+    int qblk, bh;
+    dispatch_order(nqb, H, DENSE ? nullptr : reinterpret_cast<const int4*>(a.qsum), Lp / 32, (L + 31) / 32, W,
+                   false, (int64_t)4 * L * D * sizeof(T), 4 << 20, qblk, bh);
     const int b = bh / H, h = bh % H;
     const int qw0 = qblk * 32 * W + wave * 32;
     const int q = qw0 + ql;

@@ -255,8 +255,10 @@ void fwd_kernel(const FwdArgs args) {
     const int ql = lane & 31, hh = lane >> 5;
     const int L = p.L, H = p.H, Lp = args.Lp;
     const int nqb = (L + QW * W - 1) / (QW * W);
-    const int g = xcd_remap(blockIdx.x, gridDim.x);
-    const int qb = g % nqb, bh = g / nqb;
+    // Query blocks whose rows straddle a chain boundary are dispatched first.
+    int qb, bh;
+    dispatch_order(nqb, H, DENSE ? nullptr : reinterpret_cast<const int4*>(args.qsum), Lp / 32,
+                   (L + 31) / 32, QB * W, false, (int64_t)4 * L * D * sizeof(T), 2 << 20, qb, bh);
     const int b = bh / H, h = bh % H;
     const int qw0 = qb * QW * W;    // first query of the workgroup
     const int qv0 = qw0 + wave * QW;  // first query of this wavefront

@@ -90,6 +90,18 @@ def test_bwd_chain_counts(nchains):
     assert_grads(got, ref, f"nchains={nchains}")
 
 
+@pytest.mark.parametrize("B,H,L,D,nchains", [(2, 4, 1000, 32, 3), (2, 4, 512, 64, 2)])
+def test_bwd_heavy_first_dispatch(B, H, L, D, nchains):
+    """Grids that divide evenly over the 8 XCDs take the dispatch order with
+    two-chain (and, for dK/dV, padded) blocks first: every block must still
+    be computed exactly once."""
+    print(f"[bwd dispatch] B={B} H={H} L={L} D={D} chains={nchains}", flush=True)
+    xs, go, cid, kp = make_inputs(B, H, L, D, torch.bfloat16, seed=B * L + D, nchains=nchains)
+    got = run_gpu(xs, go, cid, kp, rope=True, scale=D ** -0.5)
+    ref = oracle_grads(xs, go, cid, kp, rope=True, scale=D ** -0.5)
+    assert_grads(got, ref, f"dispatch B={B} H={H} L={L} D={D}")
+
+
 @pytest.mark.parametrize("D", [32, 64])
 def test_bwd_no_rope_dense_mask(D):
     """Reference contract: no fused RoPE, scale 1, dense (B, L, L) mask."""

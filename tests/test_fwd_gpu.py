@@ -113,6 +113,19 @@ def test_fwd_chain_counts(nchains):
     assert_close16(got, ref, f"nchains={nchains}")
 
 
+@pytest.mark.parametrize("B,H,L,D,nchains", [(2, 4, 1000, 32, 3), (4, 4, 512, 32, 2),
+                                             (2, 4, 900, 16, 4), (2, 8, 512, 64, 3)])
+def test_fwd_heavy_first_dispatch(B, H, L, D, nchains):
+    """Grids that divide evenly over the 8 XCDs take the dispatch order with
+    chain-straddling workgroups first (the others the plain order): every
+    (b, h, query block) must still be computed exactly once."""
+    print(f"[fwd dispatch] B={B} H={H} L={L} D={D} chains={nchains}", flush=True)
+    xs, cid, kp = make_inputs(B, H, L, D, torch.bfloat16, seed=B * L + D, nchains=nchains)
+    got = run_gpu(xs, cid, kp, rope=True, scale=D ** -0.5)
+    ref = oracle_out(xs, cid, kp, rope=True, scale=D ** -0.5)
+    assert_close16(got, ref, f"dispatch B={B} H={H} L={L}")
+
+
 def test_fwd_prerotated_contract():
     """Reference contract: q pre-scaled, q/k pre-rotated, scale 1, dense mask."""
     print("[fwd prerotated dense]", flush=True)
