@@ -168,10 +168,21 @@ class TransformerLayer_MINT(nn.Module):
         out = out.transpose(1, 2).reshape(B, T, E)
         return self.self_attn.out_proj(out).transpose(0, 1).contiguous(), None
 
+    def _fused_covers(self, x):
+        """The fused kernels serve 16-bit inputs in training and inference,
+        fp32 inputs for inference without dropout (the fp32 fused backward
+        and fp32 dropout are not built; the combine kernels cover them)."""
+        if x.dtype != torch.float32:
+            return True
+        sa, ma = self.self_attn, self.multimer_attn
+        grad = torch.is_grad_enabled() and (x.requires_grad or _needs_grad(sa, ma))
+        return not grad and not (self.training and sa.dropout > 0)
+
     def _multimer_attention_plus(self, x, chain_mask, padding_mask, chain_ids=None):
         """Dispatch (modules.py:200-249): fused multi-pathway kernel when the
-        flag is set, else the materialised pipeline with the combine kernel."""
-        if self._use_fused_multi_pathway:
+        flag is set (and it covers the dtype and mode), else the materialised
+        pipeline with the combine kernel."""
+        if self._use_fused_multi_pathway and self._fused_covers(x):
             return self._multimer_attention_superfused(x, chain_mask, padding_mask, chain_ids)
         if getattr(self, "_use_eager_multimer", False):
             return self._multimer_attention(x, chain_mask, padding_mask, chain_ids)
