@@ -81,36 +81,30 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
     return xcd * per + (xcd < rem ? xcd : rem) + slot;
 }
 
-// Workgroup -> (row block, b*H + h) for grids of nblk_bh row blocks per
-// (b, h). Each XCD takes a contiguous share of whole (b, h) groups, as
-// xcd_remap does. When the grid splits evenly over the XCDs and `sums` is
-// given (one int4 {min chain, max chain, #padded, -} per 32 rows of each
-// batch row, `nsum` of them valid, `rows32` of them per workgroup), the
-// share is walked in runs of a few groups whose shared operands
-// (`group_bytes` each) fit together in `budget` bytes of the XCD's L2, and
-// inside a run the
-// workgroups whose rows span two chains (about twice the work per stage;
-// with pad_heavy also those holding padded rows) are dispatched first, so
+// Position `slot` of the share of XCD `xcd` -> (row block, b*H + h), for
+// nblk_bh row blocks per (b, h) and ngrp whole (b, h) groups per share (the
+// share of XCD x is groups [x*ngrp, (x+1)*ngrp), so their shared operands
+// stay in that XCD's L2). The share is walked in runs of a few groups whose
+// shared operands (`group_bytes` each) fit together in `budget` bytes of
+// L2. With `sums` (one int4 {min chain, max chain, #padded, -} per 32 rows
+// of each batch row, `nsum` of them valid, `rows32` of them per block),
+// inside a run the blocks whose rows span two chains (about twice the work
+// per stage; with pad_heavy also those holding padded rows) come first, so
 // they overlap the others instead of extending the last round. Results are
 // wavefront-uniform.
-__device__ inline void dispatch_order(int nblk_bh, int H, const int4* sums, int64_t sums_per_b, int nsum,
-                                      int rows32, bool pad_heavy, int64_t group_bytes, int64_t budget,
-                                      int& blk, int& bh) {
-    constexpr int kXcd = 8;
-    const int nblk = gridDim.x, bid = blockIdx.x;
-    const int per = nblk / kXcd;
-    if (sums && nblk % kXcd == 0 && per % nblk_bh == 0 && nblk_bh > 1 && nblk_bh <= 64) {
+__device__ inline void order_in_share(int xcd, int slot, int nblk_bh, int ngrp, int H, const int4* sums,
+                                      int64_t sums_per_b, int nsum, int rows32, bool pad_heavy,
+                                      int64_t group_bytes, int64_t budget, int& blk, int& bh) {
+    // run length: a divisor of ngrp, at most `budget` bytes of shared operands
+    int run = (int)min<int64_t>(ngrp, max<int64_t>(1, budget / max<int64_t>(group_bytes, 1)));
+    while (ngrp % run) --run;
+    const int r0 = slot / (run * nblk_bh), in = slot % (run * nblk_bh);
+    bh = xcd * ngrp + r0 * run + in % run;
+    const int rank = in / run;  // position inside the group
+    uint64_t heavy = 0;
+    if (sums && nblk_bh <= 64) {
         const int lane = threadIdx.x & 63;
-        const int xcd = bid % kXcd, slot = bid / kXcd;
-        const int ngrp = per / nblk_bh;  // (b, h) groups per XCD
-        // run length: a divisor of ngrp, at most `budget` bytes of shared operands
-        int run = (int)min<int64_t>(ngrp, max<int64_t>(1, budget / max<int64_t>(group_bytes, 1)));
-        while (ngrp % run) --run;
-        const int r0 = slot / (run * nblk_bh), in = slot % (run * nblk_bh);
-        bh = xcd * ngrp + r0 * run + in % run;
-        const int rank = in / run;  // dispatch rank inside the group
         const int4* sb = sums + (int64_t)(bh / H) * sums_per_b;
-        uint64_t heavy = 0;
         for (int c0 = 0; c0 < nsum; c0 += 64) {
             bool two = false;
             if (c0 + lane < nsum) {
@@ -123,17 +117,36 @@ __device__ inline void dispatch_order(int nblk_bh, int H, const int4* sums, int6
                 bits &= bits - 1;
             }
         }
-        const int nh = __builtin_popcountll(heavy);
+    }
+    const int nh = __builtin_popcountll(heavy);
+    if (nblk_bh > 64 || nh == 0) {
+        blk = rank;
+    } else {
         uint64_t pool = rank < nh ? heavy : ~heavy & (nblk_bh == 64 ? ~0ull : (1ull << nblk_bh) - 1);
         for (int k = rank < nh ? rank : rank - nh; k > 0; --k) pool &= pool - 1;
         blk = __builtin_ctzll(pool);
-    } else {
-        const int g = xcd_remap(bid, nblk);
-        blk = g % nblk_bh;
-        bh = g / nblk_bh;
     }
     blk = __builtin_amdgcn_readfirstlane(blk);
     bh = __builtin_amdgcn_readfirstlane(bh);
+}
+
+// Workgroup -> (row block, b*H + h) for a grid of one workgroup per block:
+// order_in_share over the XCD shares when the grid splits evenly over the 8
+// XCDs (dispatch is round-robin over them), else xcd_remap's order.
+__device__ inline void dispatch_order(int nblk_bh, int H, const int4* sums, int64_t sums_per_b, int nsum,
+                                      int rows32, bool pad_heavy, int64_t group_bytes, int64_t budget,
+                                      int& blk, int& bh) {
+    constexpr int kXcd = 8;
+    const int nblk = gridDim.x, bid = blockIdx.x;
+    const int per = nblk / kXcd;
+    if (nblk % kXcd == 0 && per % nblk_bh == 0) {
+        order_in_share(bid % kXcd, bid / kXcd, nblk_bh, per / nblk_bh, H, sums, sums_per_b, nsum, rows32,
+                       pad_heavy, group_bytes, budget, blk, bh);
+    } else {
+        const int g = xcd_remap(bid, nblk);
+        blk = __builtin_amdgcn_readfirstlane(g % nblk_bh);
+        bh = __builtin_amdgcn_readfirstlane(g / nblk_bh);
+    }
 }
 
 __device__ __forceinline__ float wave_max(float v) {
