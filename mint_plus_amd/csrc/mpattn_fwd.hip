@@ -17,9 +17,10 @@
 //    the logit scale applied in fp32.
 //  * Keys stream through a ring of NBUF LDS stages of 64 keys. A stage has
 //    room for K_self, K_multi, V_self, V_multi tiles, copied by
-//    global_load_lds (16 bytes per lane, straight into LDS); only the tiles of
-//    the pathways some wavefront of the workgroup needs are copied. Copies run
-//    NBUF-1 stages ahead; one barrier per stage. Rows are stored densely with
+//    global_load_lds (16 bytes per lane, straight into LDS); all four are
+//    copied (skipping the tiles no wavefront needs saved L2 reads but cost
+//    more in branches than it saved). Copies run NBUF-1 stages ahead; one
+//    barrier per stage. Rows are stored densely with
 //    their 16-byte chunks XOR-swizzled by row to spread LDS banks.
 //  * Per 32-key subtile a wavefront computes S^T = K Q^T with
 //    v_mfma_f32_32x32x16 (rows = keys, columns = queries): lane l holds 16
@@ -324,11 +325,11 @@ void fwd_kernel(const FwdArgs args) {
     const unsigned smem_base = lds_addr(smem);
     const unsigned scid_base = lds_addr(&scid[wave][0][0]);
 
-    // ---- copy stage s into buffer bf: only the pathways the workgroup needs ----
+    // ---- copy stage s into buffer bf ----
     // Returns the number of vector-memory instructions issued (uniform).
     // Source rows are addressed per lane (64-bit): the row offset of a stage
     // is s * 64 * stride, below 2^31 bytes (checked on the host).
-    auto issue = [&](int s, int bf, int tiles) -> int {
+    auto issue = [&](int s, int bf) -> int {
         const int k0 = s * kBN;
         const unsigned lb = smem_base + bf * S::STAGE;
         const char* va[NJ];
@@ -351,7 +352,7 @@ void fwd_kernel(const FwdArgs args) {
         int n = 1;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-            if ((tiles >> dten[j]) & 1) {
+            if (TOT % W == 0 || dten[j] < 4) {  // (idle copies of the last round)
                 dma16v(va[j], lb + dlds[j]);
                 ++n;
             }
@@ -360,14 +361,12 @@ void fwd_kernel(const FwdArgs args) {
         return n;
     };
 
-    // Stage 0 is copied first, with every tile, so its copy overlaps the
-    // prologue loads below instead of waiting for the chain summaries that
-    // decide which tiles later stages need.
+    // Stage 0 is copied first, so its copy overlaps the prologue loads below.
     const int nst = (L + kBN - 1) / kBN;
     int pend[NBUF];
 #pragma unroll
     for (int t = 0; t < NBUF; ++t) pend[t] = 0;
-    pend[0] = issue(0, 0, 15);
+    pend[0] = issue(0, 0);
 
     // ---- Q fragments (B operand of S^T = K Q^T): dims kk*16 + 8*hh + [0,8) ----
     v8 qf[QB][2][S::NKK];
@@ -389,32 +388,22 @@ void fwd_kernel(const FwdArgs args) {
                 }
                 qf[u][pw][kk] = pack8<T>(x);
             }
-    // Query chain ranges of each block and of the whole workgroup
-    // (from the per-32-query summaries of the prep kernel: uniform loads).
+    // Query chain range of each block (the prep kernel's per-32-query
+    // summaries: uniform loads).
     int cq[QB], cq_min[QB], cq_max[QB];
-    int wq_min = INT32_MAX, wq_max = INT32_MIN;
 #pragma unroll
     for (int u = 0; u < QB; ++u) cq[u] = cq_min[u] = cq_max[u] = 0;
     if constexpr (!DENSE) {
 #pragma unroll
         for (int u = 0; u < QB; ++u) cq[u] = qvalid[u] ? p.chain_id[(int64_t)b * L + qrow[u]] : 0;
-        const int4* qsum_b = reinterpret_cast<const int4*>(args.qsum) + (int64_t)b * (Lp / 32) + qw0 / 32;
+        const int4* qsum_b = reinterpret_cast<const int4*>(args.qsum) + (int64_t)b * (Lp / 32);
 #pragma unroll
-        for (int w = 0; w < W * QB; ++w) {
-            const int4 qs = qsum_b[w < Lp / 32 - qw0 / 32 ? w : 0];
-            if (qw0 + 32 * w < L) {
-                wq_min = min(wq_min, qs.x);
-                wq_max = max(wq_max, qs.y);
-            }
-#pragma unroll
-            for (int u = 0; u < QB; ++u)
-                if (w == wave * QB + u) {
-                    cq_min[u] = qs.x;
-                    cq_max[u] = qs.y;
-                }
+        for (int u = 0; u < QB; ++u) {
+            const int qbk = (qv0 >> 5) + u;  // this block's summary (a block past L reads block 0)
+            const int4 qs = qsum_b[qbk < Lp / 32 ? qbk : 0];
+            cq_min[u] = qs.x;
+            cq_max[u] = qs.y;
         }
-        wq_min = __builtin_amdgcn_readfirstlane(wq_min);
-        wq_max = __builtin_amdgcn_readfirstlane(wq_max);
 #pragma unroll
         for (int u = 0; u < QB; ++u) {
             cq_min[u] = __builtin_amdgcn_readfirstlane(cq_min[u]);
@@ -814,11 +803,10 @@ void fwd_kernel(const FwdArgs args) {
     };
 
     // Subtile codes of each block for the 64 subtiles from kb0, as three bit
-    // masks per block (mb0..mb2 = code bits), and which pathways the workgroup
-    // needs there (nS / nM) so stages copy only those tiles. Each reload is a
-    // vector load whose wait also drains the copies in flight: windows move
-    // once per 32 stages.
-    uint64_t mb0[QB], mb1[QB], mb2[QB], nS = 0, nM = 0;
+    // masks per block (mb0..mb2 = code bits). Each reload is a vector load
+    // whose wait also drains the copies in flight: windows move once per 32
+    // stages.
+    uint64_t mb0[QB], mb1[QB], mb2[QB];
     auto ksum_at = [&](int kb0) -> int4 {
         const int kb = kb0 + lane;
         int4 sm = {0, 0, 32, 0};
@@ -834,31 +822,16 @@ void fwd_kernel(const FwdArgs args) {
             mb2[u] = __builtin_amdgcn_ballot_w64((code >> 2) & 1);
         }
     };
-    auto set_needs = [&](const int4 sm) {
-        bool ns = false, nm = false;
-        if (sm.z < 32) {
-            if (DENSE || sm.z > 0) {
-                ns = nm = true;
-            } else {
-                ns = !(sm.y < wq_min || sm.x > wq_max);
-                nm = !(sm.x == sm.y && wq_min == wq_max && sm.x == wq_min);
-            }
-        }
-        nS = __builtin_amdgcn_ballot_w64(ns);
-        nM = __builtin_amdgcn_ballot_w64(nm);
-    };
     // Control words of a window of 32 stages, one per lane (lane t: stage
     // sw0 + t): the codes of the stage's two subtiles for each query block
-    // (3 bits each, block u from bit 6u) and, from bit 12, the tiles the stage
-    // copies. Built once per window, read with one readlane per stage. A
-    // rebuild's summary load waits for the copies in flight; windows move
-    // once per 32 stages.
+    // (3 bits each, block u from bit 6u). Built once per window, read with
+    // one readlane per stage. A rebuild's summary load waits for the copies
+    // in flight; windows move once per 32 stages.
     int ctrl = 0, sw0 = 0;
     auto build_ctrl = [&](int s0) {
         sw0 = s0;
         const int4 sm = ksum_at(2 * s0);  // lane: subtile 2*s0 + lane
         set_codes(sm);
-        set_needs(sm);
         const int t2 = 2 * (lane & 31);
         int w = 0;
 #pragma unroll
@@ -869,8 +842,7 @@ void fwd_kernel(const FwdArgs args) {
                            (int)(((mb2[u] >> (t2 + 1)) & 1) << 2);
             w |= (a | bb << 3) << (6 * u);
         }
-        const int tl = (((nS >> t2) & 3) != 0 ? 5 : 0) | (((nM >> t2) & 3) != 0 ? 10 : 0);
-        ctrl = w | tl << 12;
+        ctrl = w;
     };
 
     // ---- main loop over stages ----
@@ -881,15 +853,11 @@ void fwd_kernel(const FwdArgs args) {
     // drain the copies in flight.
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     pend[0] = 0;
-    // Tiles stage t copies (bit i = tile i): K_self and V_self (bits 0, 2)
-    // if any of its subtiles needs the self pathway, K_multi and V_multi
-    // (1, 3) for the multimer pathway.
-    auto tiles_of = [&](int t) -> int { return __builtin_amdgcn_readlane(ctrl, t - sw0) >> 12; };
     // pend[k]: vector-memory instructions of stage s + k still in flight
     // (stage 0 was issued before the prologue and has landed).
 #pragma unroll
     for (int t = 1; t < NBUF - 1; ++t)
-        if (t < nst) pend[t] = issue(t, t, tiles_of(t));
+        if (t < nst) pend[t] = issue(t, t);
     int bf = 0;
     for (int s = 0; s < nst; ++s) {
         int allow = 0;  // copies of later stages that may stay in flight
@@ -910,7 +878,7 @@ void fwd_kernel(const FwdArgs args) {
         }
         if (s + NBUF - 1 < nst) {
             const int bn = bf + NBUF - 1 >= NBUF ? bf - 1 : bf + NBUF - 1;
-            pend[NBUF - 2] = issue(s + NBUF - 1, bn, tiles_of(s + NBUF - 1));
+            pend[NBUF - 2] = issue(s + NBUF - 1, bn);
         }
 
         const char* stage = smem + bf * S::STAGE;
