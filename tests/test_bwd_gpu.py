@@ -90,14 +90,16 @@ def test_bwd_chain_counts(nchains):
     assert_grads(got, ref, f"nchains={nchains}")
 
 
-@pytest.mark.parametrize("B,H,L,D,nchains", [(2, 4, 1000, 32, 3), (2, 4, 512, 64, 2)])
-def test_bwd_heavy_first_dispatch(B, H, L, D, nchains):
+@pytest.mark.parametrize("B,H,L,D,nchains,dense", [(2, 4, 1000, 32, 3, False), (2, 4, 512, 64, 2, False),
+                                                   (2, 4, 1000, 32, 3, True)])
+def test_bwd_heavy_first_dispatch(B, H, L, D, nchains, dense):
     """Grids that divide evenly over the 8 XCDs take the dispatch order with
-    two-chain (and, for dK/dV, padded) blocks first: every block must still
-    be computed exactly once."""
-    print(f"[bwd dispatch] B={B} H={H} L={L} D={D} chains={nchains}", flush=True)
+    two-chain (and, for dK/dV, padded) blocks first (dense mask: the plain
+    order inside each XCD's share): every block must still be computed
+    exactly once."""
+    print(f"[bwd dispatch] B={B} H={H} L={L} D={D} chains={nchains} dense={dense}", flush=True)
     xs, go, cid, kp = make_inputs(B, H, L, D, torch.bfloat16, seed=B * L + D, nchains=nchains)
-    got = run_gpu(xs, go, cid, kp, rope=True, scale=D ** -0.5)
+    got = run_gpu(xs, go, cid, kp, rope=True, scale=D ** -0.5, dense=dense)
     ref = oracle_grads(xs, go, cid, kp, rope=True, scale=D ** -0.5)
     assert_grads(got, ref, f"dispatch B={B} H={H} L={L} D={D}")
 

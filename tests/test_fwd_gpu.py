@@ -113,17 +113,19 @@ def test_fwd_chain_counts(nchains):
     assert_close16(got, ref, f"nchains={nchains}")
 
 
-@pytest.mark.parametrize("B,H,L,D,nchains", [(2, 4, 1000, 32, 3), (4, 4, 512, 32, 2),
-                                             (2, 4, 900, 16, 4), (2, 8, 512, 64, 3)])
-def test_fwd_heavy_first_dispatch(B, H, L, D, nchains):
+@pytest.mark.parametrize("B,H,L,D,nchains,dense", [(2, 4, 1000, 32, 3, False), (4, 4, 512, 32, 2, False),
+                                                   (2, 4, 900, 16, 4, False), (2, 8, 512, 64, 3, False),
+                                                   (2, 4, 1000, 32, 3, True)])
+def test_fwd_heavy_first_dispatch(B, H, L, D, nchains, dense):
     """Grids that divide evenly over the 8 XCDs take the dispatch order with
-    chain-straddling workgroups first (the others the plain order): every
-    (b, h, query block) must still be computed exactly once."""
-    print(f"[fwd dispatch] B={B} H={H} L={L} D={D} chains={nchains}", flush=True)
+    chain-straddling workgroups first (with a dense mask: the plain order
+    inside each XCD's share; other grids: xcd_remap's order): every (b, h,
+    query block) must still be computed exactly once."""
+    print(f"[fwd dispatch] B={B} H={H} L={L} D={D} chains={nchains} dense={dense}", flush=True)
     xs, cid, kp = make_inputs(B, H, L, D, torch.bfloat16, seed=B * L + D, nchains=nchains)
-    got = run_gpu(xs, cid, kp, rope=True, scale=D ** -0.5)
+    got = run_gpu(xs, cid, kp, rope=True, scale=D ** -0.5, dense=dense)
     ref = oracle_out(xs, cid, kp, rope=True, scale=D ** -0.5)
-    assert_close16(got, ref, f"dispatch B={B} H={H} L={L}")
+    assert_close16(got, ref, f"dispatch B={B} H={H} L={L} dense={dense}")
 
 
 def test_fwd_prerotated_contract():
