@@ -151,11 +151,12 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--mode", choices=("fwd", "fwdbwd", "model", "attn3b", "combine"),
+    ap.add_argument("--mode", choices=("fwd", "fwdbwd", "model", "attn3b", "attn650m", "combine"),
                     default="fwd",
                     help="fwd: the headline forward (B=16); fwdbwd: forward + backward at the "
                          "training shape (B=8, dO ~ N(0, 1)); model: 650M MINT forward "
-                         "sequences/s per attention path; attn3b: the op at the 3B shape; "
+                         "sequences/s per attention path; attn3b / attn650m: the op at the 3B / "
+                         "650M model's attention shape; "
                          "combine: the materialised-logit combine fwd and bwd (HBM-bound)")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the 650M model forward summary of the default line")
@@ -194,8 +195,8 @@ def main():
         print(json.dumps(bench_model(dev, steps=max(3, min(args.steps, 10)),
                                      warmup=min(args.warmup, 3))), flush=True)
         return
-    if args.mode == "attn3b":
-        return bench_attn3b(args, dev)
+    if args.mode in ("attn3b", "attn650m"):
+        return bench_attn_shape(args, dev, args.mode[4:])
     if args.mode == "combine":
         return bench_combine(args, dev)
     xs, cid, pad = make_workload(dev)
@@ -341,25 +342,44 @@ def bench_fwdbwd(args, dev):
     print(json.dumps(res), flush=True)
 
 
-def bench_attn3b(args, dev):
-    """The op at the 3B attention shape: B=4, H=40, D=64, three chains of
-    ~U[200, 800] tokens with L_total <= 2048, padded to 2048."""
-    from mint_plus_amd import _lib
-    b, h, l, d = 4, 40, 2048, 64
+def attn_shape_inputs(dev, shape):
+    """Inputs of the op at a model's attention shape (bf16, N(0, 1/D)).
+
+    3b: B=4, H=40, D=64, three chains of ~U[200, 800] tokens with
+    L_total <= 2048, padded to 2048.
+    650m: B=8, H=20, D=64, the 650M model's batch (two chains, L_total
+    ~U[512, 1024], each chain >= 64, padded to the batch max; configs[2])."""
     g = torch.Generator(device="cpu").manual_seed(3000)
+    if shape == "3b":
+        b, h, l, d = 4, 40, 2048, 64
+        cid = torch.full((b, l), 2, dtype=torch.int32)
+        pad = torch.zeros(b, l, dtype=torch.bool)
+        for i in range(b):
+            while True:
+                n = [int(torch.randint(200, 801, (1,), generator=g)) for _ in range(3)]
+                if sum(n) <= l:
+                    break
+            cid[i, :n[0]] = 0
+            cid[i, n[0]:n[0] + n[1]] = 1
+            pad[i, sum(n):] = True
+        data = "synthetic (3 chains ~U[200,800], padded to 2048)"
+    else:
+        b, h, d = 8, 20, 64
+        tok, cid = model_batch("cpu", 650, b, 512, 1024, 64)
+        l = int(tok.shape[1])
+        cid = cid.to(torch.int32)
+        pad = tok == 1
+        data = f"synthetic (2 chains, L_total ~U[512,1024], padded to {l})"
     xs = [(torch.randn(b, h, l, d, generator=g) / d ** 0.5).to(torch.bfloat16).to(dev)
           for _ in range(6)]
-    cid = torch.full((b, l), 2, dtype=torch.int32)
-    pad = torch.zeros(b, l, dtype=torch.bool)
-    for i in range(b):
-        while True:
-            n = [int(torch.randint(200, 801, (1,), generator=g)) for _ in range(3)]
-            if sum(n) <= l:
-                break
-        cid[i, :n[0]] = 0
-        cid[i, n[0]:n[0] + n[1]] = 1
-        pad[i, sum(n):] = True
-    cid, pad = cid.to(dev), pad.to(dev)
+    return xs, cid.to(dev), pad.to(dev), (b, h, l, d), data
+
+
+def bench_attn_shape(args, dev, shape):
+    """The op (forward, fused RoPE) at the 3B or 650M model's attention
+    shape: TFLOP/s on the algorithmic 4*B*H*L^2*D."""
+    from mint_plus_amd import _lib
+    xs, cid, pad, (b, h, l, d), data = attn_shape_inputs(dev, shape)
     out = torch.empty_like(xs[0])
 
     def step():
@@ -370,14 +390,16 @@ def bench_attn3b(args, dev):
     wall, per = timed(step, args.steps, args.warmup, stream)
     med = statistics.median(per)
     fl = 4.0 * b * h * l * l * d
+    name = {"3b": "3B", "650m": "650M"}[shape]
     print(json.dumps({
-        "metric": "multi-pathway attn fwd TFLOP/s (3B shape, bf16)",
+        "metric": f"multi-pathway attn fwd TFLOP/s ({name} shape, bf16)",
         "value": round(fl / (med * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(wall * 1e3 / args.steps, 5), "higher_is_better": True,
-        "dtype": "bf16", "data": "synthetic (3 chains ~U[200,800], padded to 2048)",
-        "config": {"workload": "3B-shape multi-pathway attention forward (one layer)",
-                   "B": b, "H": h, "L": l, "D": d, "rope": "fused", "chains": 3},
+        "dtype": "bf16", "data": data,
+        "config": {"workload": f"{name}-shape multi-pathway attention forward (one layer)",
+                   "B": b, "H": h, "L": l, "D": d, "rope": "fused",
+                   "chains": 3 if shape == "3b" else 2},
         "kernel_ms": {"median": round(med, 5), "p10": round(per[len(per) // 10], 5),
                       "p90": round(per[(9 * len(per)) // 10], 5)},
         "pct_bf16_peak": round(100.0 * fl / (med * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),

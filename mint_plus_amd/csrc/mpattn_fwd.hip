@@ -291,11 +291,13 @@ void fwd_kernel(const FwdArgs args) {
     // ---- DMA plan: copy j of this wavefront covers 16-byte slots
     // [64*part, 64*part + 64) of tile `ten` (0 K_self, 1 K_multi, 2 V_self,
     // 3 V_multi); lane -> (row r, logical chunk c), physical slot swizzled.
+    // When W divides a tile's instruction count, copy j's tile is j*W/NI for
+    // every wavefront (a compile-time constant).
+    constexpr bool TSTAT = S::NI % W == 0;
     const char* dsb[NJ];  // (b, h) base of the source tensor (uniform)
     unsigned dstr[NJ];    // row stride in bytes (uniform)
-    unsigned dinc[NJ];    // bytes between stages: 64 rows (uniform)
     unsigned dlds[NJ];    // LDS offset inside a stage (uniform)
-    const char* dva[NJ];  // per-lane source address of (r, c) in stage 0
+    unsigned dvo[NJ];     // per-lane byte offset of (r, c) from the stage's first row
     int dten[NJ];         // tile index, 4 for an idle copy (uniform)
     // (row, swizzled byte column) of copy j for lane `ln`
     auto dma_rc = [&](int j, int ln, int& r, int& cb) {
@@ -309,34 +311,44 @@ void fwd_kernel(const FwdArgs args) {
     for (int j = 0; j < NJ; ++j) {
         const int ins0 = wave + j * W;
         const int ins = ins0 < TOT ? ins0 : TOT - 1;
-        const int ten = ins / S::NI, part = ins % S::NI;
+        const int ten = TSTAT ? j * W / S::NI : ins / S::NI;
+        const int part = TSTAT ? j * W % S::NI + wave : ins % S::NI;
         int r, cb;
         dma_rc(j, lane, r, cb);
         const T* tb = ten == 0 ? ks_p : ten == 1 ? km_p : ten == 2 ? vs_p : vm_p;
         const int64_t ts = ten == 0 ? ks_t : ten == 1 ? km_t : ten == 2 ? vs_t : vm_t;
         dsb[j] = (const char*)tb;
         dstr[j] = (unsigned)(ts * (int64_t)sizeof(T));
-        dinc[j] = dstr[j] * kBN;
         dlds[j] = ten * S::TILE + part * 1024;
-        dva[j] = dsb[j] + (r * dstr[j] + cb);
+        dvo[j] = r * dstr[j] + cb;
         dten[j] = ins0 < TOT ? ten : 4;
     }
-    const char* const keff_lane = reinterpret_cast<const char*>(keff_b) + lane * 4;
+    const char* const keff_c = reinterpret_cast<const char*>(keff_b);
     const unsigned smem_base = lds_addr(smem);
     const unsigned scid_base = lds_addr(&scid[wave][0][0]);
 
     // ---- copy stage s into buffer bf ----
     // Returns the number of vector-memory instructions issued (uniform).
-    // Source rows are addressed per lane (64-bit): the row offset of a stage
-    // is s * 64 * stride, below 2^31 bytes (checked on the host).
+    // Sources are a uniform 64-bit base (the stage's first row, advanced by
+    // scalar adds) plus a per-lane 32-bit offset inside the stage's 64 rows:
+    // no per-lane address arithmetic per stage.
     auto issue = [&](int s, int bf) -> int {
         const int k0 = s * kBN;
         const unsigned lb = smem_base + bf * S::STAGE;
-        const char* va[NJ];
-        if (k0 + kBN <= L) {
+        // Each branch issues its own copies (no register merge of the offsets).
+        auto copies = [&](const unsigned* vo) {
+            const int m0v = m0_save();
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) va[j] = dva[j] + (unsigned)s * dinc[j];
+            for (int j = 0; j < NJ; ++j)
+                if (TOT % W == 0 || dten[j] < 4)  // (idle copies of the last round)
+                    dma16(dsb[j] + (int64_t)k0 * dstr[j], vo[j], lb + dlds[j]);
+            dma4(keff_c + k0 * 4, (unsigned)lane * 4, scid_base + bf * kBN * 4);
+            m0_restore(m0v);
+        };
+        if (k0 + kBN <= L) {
+            copies(dvo);
         } else {  // last stage: clamp rows past L to L-1 (their keys are masked)
+            unsigned vo[NJ];
             // The lane id comes from an opaque instruction so that (r, cb)
             // are recomputed here instead of occupying registers all loop.
             int ln;
@@ -345,19 +357,13 @@ void fwd_kernel(const FwdArgs args) {
             for (int j = 0; j < NJ; ++j) {
                 int r, cb;
                 dma_rc(j, ln, r, cb);
-                va[j] = dsb[j] + ((unsigned)min(k0 + r, L - 1) * dstr[j] + cb);
+                vo[j] = (unsigned)min(r, L - 1 - k0) * dstr[j] + cb;
             }
+            copies(vo);
         }
-        const int m0v = m0_save();
         int n = 1;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
-            if (TOT % W == 0 || dten[j] < 4) {  // (idle copies of the last round)
-                dma16v(va[j], lb + dlds[j]);
-                ++n;
-            }
-        dma4v(keff_lane + k0 * 4, scid_base + bf * kBN * 4);
-        m0_restore(m0v);
+        for (int j = 0; j < NJ; ++j) n += (TOT % W == 0 || dten[j] < 4) ? 1 : 0;
         return n;
     };
 
@@ -903,12 +909,11 @@ void fwd_kernel(const FwdArgs args) {
             for_blocks<QB>([&](auto u_c) {
                 constexpr int u = decltype(u_c)::value;
                 if ((done >> u) & 1) return;
-                // Unrolled for chain ids and D <= 32: with an inner loop the
-                // accumulators get a second register home and every fast
-                // stage pays two copies of them. D = 64 and the dense-mask
-                // kernels keep the loop (unrolled, they spill or no longer fit
-                // their occupancy).
-                if constexpr (D == 64 || DENSE) {
+                // Unrolled for chain ids: with an inner loop the accumulators
+                // get a second register home and every fast stage pays two
+                // copies of them. The dense-mask kernels keep the loop
+                // (unrolled, they no longer fit their occupancy).
+                if constexpr (DENSE) {
 #pragma unroll 1
                     for (int st = 0; st < 2; ++st) slow_subtile(u_c, stage, cid, st, st ? c1[u] : c0[u], k0);
                 } else {
