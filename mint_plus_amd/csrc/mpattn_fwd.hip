@@ -367,15 +367,48 @@ void fwd_kernel(const FwdArgs args) {
         return n;
     };
 
-    // Stage 0 is copied first, so its copy overlaps the prologue loads below.
     const int nst = (L + kBN - 1) / kBN;
     int pend[NBUF];
 #pragma unroll
     for (int t = 0; t < NBUF; ++t) pend[t] = 0;
-    pend[0] = issue(0, 0);
-
     // ---- Q fragments (B operand of S^T = K Q^T): dims kk*16 + 8*hh + [0,8) ----
+    // With D/2 a multiple of 8 the raw Q rows (with the RoPE partner chunks
+    // and table entries) are loaded first and the stage-0 copy is issued
+    // behind them: both are in flight together, and the loads are not queued
+    // behind the copy (3-5 % of the call at D = 32 and 64).
+    constexpr int H2 = D / 2;
+    constexpr bool QEARLY = H2 % 8 == 0;
     v8 qf[QB][2][S::NKK];
+    v8 qraw[QB][2][S::NKK], qpar[QB][S::NKK];
+    f32x4 qcs[QB][S::NKK][4];
+    if constexpr (QEARLY) {
+#pragma unroll
+        for (int u = 0; u < QB; ++u) {
+            const int qr = qvalid[u] ? qrow[u] : 0;
+#pragma unroll
+            for (int pw = 0; pw < 2; ++pw)
+#pragma unroll
+                for (int kk = 0; kk < S::NKK; ++kk) {
+                    const int d0 = kk * 16 + hh * 8;
+                    if (d0 >= D) continue;
+                    const T* row = pw == 0 ? qs_p + (int64_t)qr * p.q_self.stride_t
+                                           : qm_p + (int64_t)qr * p.q_multi.stride_t;
+                    qraw[u][pw][kk] = *reinterpret_cast<const v8*>(row + d0);
+                    if (ROPE && pw == 0) {
+                        const bool lo = d0 < H2;
+                        const int dp = lo ? d0 + H2 : d0 - H2, fi = lo ? d0 : dp;
+                        qpar[u][kk] = *reinterpret_cast<const v8*>(row + dp);
+                        const float* cr = p.rope_cos + (int64_t)qr * H2 + fi;
+                        const float* sr = p.rope_sin + (int64_t)qr * H2 + fi;
+                        qcs[u][kk][0] = *reinterpret_cast<const f32x4*>(cr);
+                        qcs[u][kk][1] = *reinterpret_cast<const f32x4*>(cr + 4);
+                        qcs[u][kk][2] = *reinterpret_cast<const f32x4*>(sr);
+                        qcs[u][kk][3] = *reinterpret_cast<const f32x4*>(sr + 4);
+                    }
+                }
+        }
+    }
+    pend[0] = issue(0, 0);
 #pragma unroll
     for (int u = 0; u < QB; ++u)
 #pragma unroll
@@ -383,7 +416,23 @@ void fwd_kernel(const FwdArgs args) {
 #pragma unroll
             for (int kk = 0; kk < S::NKK; ++kk) {
                 float x[8];
-                if (qvalid[u]) {
+                const int d0 = kk * 16 + hh * 8;
+                if (QEARLY) {
+                    if (!qvalid[u] || d0 >= D) {
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) x[t] = 0.f;
+                    } else if (ROPE && pw == 0) {
+                        const float sg = d0 < H2 ? -1.f : 1.f;
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) {
+                            const float c = qcs[u][kk][t >> 2][t & 3], sn = qcs[u][kk][2 + (t >> 2)][t & 3];
+                            x[t] = ((float)qraw[u][pw][kk][t] * c + sg * (float)qpar[u][kk][t] * sn) * args.qmul;
+                        }
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) x[t] = (float)qraw[u][pw][kk][t] * args.qmul;
+                    }
+                } else if (qvalid[u]) {
                     const T* row = pw == 0 ? qs_p + (int64_t)qrow[u] * p.q_self.stride_t
                                            : qm_p + (int64_t)qrow[u] * p.q_multi.stride_t;
                     load8_rot<T, D>(row, p.rope_cos, p.rope_sin, qrow[u], kk * 16 + hh * 8, args.qmul,
