@@ -576,19 +576,35 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     // Every wave runs every stage, also one whose keys are all padded: the
     // stage copies are split over the waves and the barriers are block-wide.
     const int nst = (L + kBS - 1) / kBS;
+    // Query summaries of a window of 64 subtiles (32 stages), one per lane,
+    // read with readlane: a summary load inside the stage would wait for
+    // the next stage's copies too. The window moves once per 32 stages.
+    auto sum_window = [&](int first) {
+        int4 v = {0, 0, 32, 0};
+        if (first + lane < Lp / 32) v = qsum_b[first + lane];
+        return v;
+    };
+    int sub0 = 0;
+    int4 qsw = sum_window(0);
     issue(0, 0);
     for (int s = 0; s < nst; ++s) {
         const int bf = s & 1;
-        wait_vm<0>();
+        // (compiler-visible: every load of the wave has landed here)
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         stage_barrier();
+        if (2 * s - sub0 >= 64) {
+            sub0 = 2 * s;
+            qsw = sum_window(sub0);
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // before the next copy is issued
+        }
         if (s + 1 < nst) issue(s + 1, bf ^ 1);
         const char* stage = smem + bf * STAGE;
         const int q0 = s * kBS;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-            const int4 qs = qsum_b[2 * s + st];
-            const int md = qmode(__builtin_amdgcn_readfirstlane(qs.x), __builtin_amdgcn_readfirstlane(qs.y),
-                                 __builtin_amdgcn_readfirstlane(qs.z));
+            const int i = 2 * s + st - sub0;
+            const int md = qmode(__builtin_amdgcn_readlane(qsw.x, i), __builtin_amdgcn_readlane(qsw.y, i),
+                                 __builtin_amdgcn_readlane(qsw.z, i));
             if (md == 0) subtile(stage, st, 0, q0);
             else if (md == 1) subtile(stage, st, 1, q0);
             else if (md == 2) subtile(stage, st, 2, q0);
@@ -880,20 +896,34 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     };
 
     const int nst = (L + kBS - 1) / kBS;
+    // Key summaries of a window of 64 subtiles (32 stages), one per lane,
+    // read with readlane (as in the dK/dV kernel).
+    auto sum_window = [&](int first) {
+        int4 v = {0, 0, 32, 0};
+        if (first + lane < Lp / 32) v = ksum_b[first + lane];
+        return v;
+    };
+    int sub0 = 0;
+    int4 ksw = sum_window(0);
     issue(0, 0);
     for (int s = 0; s < nst; ++s) {
         const int bf = s & 1;
-        wait_vm<0>();
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), compiler-visible
         stage_barrier();
+        if (2 * s - sub0 >= 64) {
+            sub0 = 2 * s;
+            ksw = sum_window(sub0);
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // before the next copy is issued
+        }
         if (s + 1 < nst) issue(s + 1, bf ^ 1);
         const char* stage = smem + bf * STAGE;
         const int* cid = &scid[wave][bf][0];
         const int k0 = s * kBS;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-            const int4 ks = ksum_b[2 * s + st];
-            const int md = kmode(__builtin_amdgcn_readfirstlane(ks.x), __builtin_amdgcn_readfirstlane(ks.y),
-                                 __builtin_amdgcn_readfirstlane(ks.z));
+            const int i = 2 * s + st - sub0;
+            const int md = kmode(__builtin_amdgcn_readlane(ksw.x, i), __builtin_amdgcn_readlane(ksw.y, i),
+                                 __builtin_amdgcn_readlane(ksw.z, i));
             if (md == 0) subtile(stage, cid, st, 0, k0);
             else if (md == 1) subtile(stage, cid, st, 1, k0);
             else if (md == 2) subtile(stage, cid, st, 2, k0);
