@@ -206,6 +206,23 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(CombineArgs a) {
     const uint32_t drow = dropon ? drop_row(a.drop.lo, (uint32_t)bh, (uint32_t)q) : 0u;
 
     const int nch = D / 8;  // 8-element chunks per value row
+    // 16-bit logits with 16-byte rows: the raw logits and mask bytes of the
+    // next 16-key step are loaded while the current step's softmax runs.
+    constexpr bool PF = VEC && !F32;
+    typedef typename OpT<T>::type rv8;
+    struct Raw {
+        rv8 i, e;
+        uint64_t m;
+    };
+    auto fetch = [&](int k, Raw& r) {
+        if (PF && k + 8 <= L) {
+            r.i = *reinterpret_cast<const rv8*>(il_row + k);
+            r.e = *reinterpret_cast<const rv8*>(el_row + k);
+            r.m = *reinterpret_cast<const uint64_t*>(m_row + k);
+        }
+    };
+    Raw nxt;
+    fetch(half * 8, nxt);
     for (int kc = 0; kc < L; kc += KC) {
         __syncthreads();
         // Stage the V tiles of both pathways (rows kc .. kc+KC-1; rows >= L
@@ -240,9 +257,23 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(CombineArgs a) {
         for (int ks = 0; ks < KC / 16; ++ks) {
             const int k = kc + ks * 16 + half * 8;
             float si[8], se[8];
-            load_logits<T, 8, VEC>(il_row, k, L, si);
-            load_logits<T, 8, VEC>(el_row, k, L, se);
-            const unsigned bits = load_mask<8, VEC>(m_row, a.m_sk, k, L);
+            unsigned bits = 0;
+            if (PF && k + 8 <= L) {
+                const Raw cur = nxt;
+                fetch(k + 16, nxt);
+                if constexpr (PF) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        si[j] = (float)cur.i[j];
+                        se[j] = (float)cur.e[j];
+                        bits |= (((cur.m >> (8 * j)) & 0xff) != 0) << j;
+                    }
+                }
+            } else {
+                load_logits<T, 8, VEC>(il_row, k, L, si);
+                load_logits<T, 8, VEC>(el_row, k, L, se);
+                bits = load_mask<8, VEC>(m_row, a.m_sk, k, L);
+            }
             float s[8];
             float cm = -INFINITY;
 #pragma unroll
