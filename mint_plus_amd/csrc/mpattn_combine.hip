@@ -400,8 +400,12 @@ __device__ __forceinline__ void store8(T* row, int k, const float v[8]) {
 // finally reads dW of its own 8 keys for the selected pathway and writes
 // dS = P (dW - Delta) into d_intra or d_inter with coalesced 16-byte stores.
 // ---------------------------------------------------------------------------
+// Register budget: 4 wavefronts per SIMD for D <= 32 (with the prefetch the
+// compiler would otherwise settle at 3; it keeps 8 bytes of scratch), 3 for
+// D = 64.
 template <typename T, int ND, bool VEC>
-__global__ __launch_bounds__(256) void combine_bwd_kernel(CombineArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ND == 1 ? 4 : 3))) void combine_bwd_kernel(
+    CombineArgs a) {
     constexpr bool F32 = sizeof(T) == 4;
     constexpr int DP = ND * 32;
     // 16-bit: P^T [2][64 keys][32 q + 8], dO^T [DP][32 + 8], dO rows [32][DP + 8].
@@ -465,20 +469,51 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(CombineArgs a) {
 
     const int nch = D / 8;
     const bool dropon = a.drop_on != 0;
+    // 16-bit logits with 16-byte rows: the next step's raw logits, mask
+    // bytes, LSE and Delta are loaded while the current step runs.
+    constexpr bool PF = VEC && !F32;
+    typedef typename OpT<T>::type rv8;
+    const bool pfk = PF && k8 + 8 <= L;
+    rv8 ni, ne;
+    uint64_t nm = 0;
+    float nl = 0.f, nd = 0.f;
+    auto fetch = [&](int q) {
+        const int qc = min(q, L - 1);
+        if (pfk) {
+            ni = *reinterpret_cast<const rv8*>(il + (int64_t)qc * a.il_st + k8);
+            ne = *reinterpret_cast<const rv8*>(el + (int64_t)qc * a.el_st + k8);
+            nm = *reinterpret_cast<const uint64_t*>(mk + (int64_t)qc * a.m_sq + k8);
+        }
+        nl = lse[qc];
+        nd = dlt[qc];
+    };
+    fetch(tq);
     for (int q0 = 0; q0 < L; q0 += 32) {
         const int qq = q0 + tq;
         const int qc = min(qq, L - 1);
         float p[8];
-        unsigned bits, keep = 0xFFu;  // keep: dropout bits of the 8 keys
+        unsigned bits = 0, keep = 0xFFu;  // keep: dropout bits of the 8 keys
         float dq;
         __syncthreads();
         {
             float si[8], se[8];
-            load_logits<T, 8, VEC>(il + (int64_t)qc * a.il_st, k8, L, si);
-            load_logits<T, 8, VEC>(el + (int64_t)qc * a.el_st, k8, L, se);
-            bits = load_mask<8, VEC>(mk + (int64_t)qc * a.m_sq, a.m_sk, k8, L);
-            const float l = lse[qc];
-            dq = dlt[qc];
+            if (pfk) {
+                if constexpr (PF) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        si[j] = (float)ni[j];
+                        se[j] = (float)ne[j];
+                        bits |= (((nm >> (8 * j)) & 0xff) != 0) << j;
+                    }
+                }
+            } else {
+                load_logits<T, 8, VEC>(il + (int64_t)qc * a.il_st, k8, L, si);
+                load_logits<T, 8, VEC>(el + (int64_t)qc * a.el_st, k8, L, se);
+                bits = load_mask<8, VEC>(mk + (int64_t)qc * a.m_sq, a.m_sk, k8, L);
+            }
+            const float l = nl;
+            dq = nd;
+            if (q0 + 32 < L) fetch(qq + 32);
             const bool ok = qq < L && l > -INFINITY;
             const float l2 = ok ? l * kLog2eC : 0.f;
             if (dropon) {
