@@ -94,6 +94,11 @@ struct BwdArgs {
 // ---------------------------------------------------------------------------
 // Prep: chain staging, Delta / LSE2 rows, RoPE of Q_self and K_self.
 // ---------------------------------------------------------------------------
+// Prep work split: lanes per row for Delta (8 dims each, a power of two) and
+// threads per row for the RoPE rotation.
+template <int D> constexpr int kPrepLanes = D <= 16 ? 2 : (D <= 32 ? 4 : 8);
+template <int D> constexpr int kRotItems = (D / 2) % 8 == 0 ? D / 16 : 1;
+
 template <typename T, int D, bool ROPE, bool DENSE>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* lse2, float* delta,
                                                        int* keff, int* ksum, int* qcid, int* qsum,
@@ -143,54 +148,89 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* l
         return;
     }
     if (bid < nchain + nrow) {
-        // One thread per (b, h, row < Lp): Delta and LSE2.
-        const int64_t row = (int64_t)(bid - nchain) * 256 + tid;
-        if (row >= (int64_t)p.B * p.H * Lp) return;
+        // Delta and LSE2 per (b, h, row < Lp): kPrepLanes<D> lanes per row,
+        // each with 8 dims, so a wave's loads cover whole rows.
+        constexpr int NPL = kPrepLanes<D>;
+        const int64_t item = (int64_t)(bid - nchain) * 256 + tid;
+        const int64_t row = item / NPL;
+        const int c = (int)(item % NPL);
+        if (row >= (int64_t)p.B * p.H * Lp) return;  // (whole row groups)
         const int t = (int)(row % Lp);
         const int bh = (int)(row / Lp);
         const int b = bh / p.H, h = bh % p.H;
-        float dl = 0.f, l2 = INFINITY;
-        if (t < L) {
+        float dl = 0.f;
+        if (t < L && c * 8 < D) {
             const T* orow = (const T*)p.out.ptr + b * p.out.stride_b + h * p.out.stride_h +
                             (int64_t)t * p.out.stride_t;
             const T* grow = (const T*)p.grad_out.ptr + b * p.grad_out.stride_b +
                             h * p.grad_out.stride_h + (int64_t)t * p.grad_out.stride_t;
+            float x[8], y[8];
+            load8f<T>(orow, c * 8, x);
+            load8f<T>(grow, c * 8, y);
 #pragma unroll
-            for (int d0 = 0; d0 < D; d0 += 8) {
-                float x[8], y[8];
-                load8f<T>(orow, d0, x);
-                load8f<T>(grow, d0, y);
-#pragma unroll
-                for (int u = 0; u < 8; ++u) dl += x[u] * y[u];
-            }
-            const float lse = p.lse[((int64_t)b * p.H + h) * L + t];
-            // A row whose keys are all padded has LSE = -inf and no probabilities.
-            l2 = lse == -INFINITY ? INFINITY : lse * a.lmul;
+            for (int u = 0; u < 8; ++u) dl += x[u] * y[u];
         }
-        lse2[row] = l2;
-        delta[row] = dl;
+#pragma unroll
+        for (int o = NPL / 2; o >= 1; o >>= 1) dl += __shfl_xor(dl, o);
+        if (c == 0) {
+            float l2 = INFINITY;
+            if (t < L) {
+                const float lse = p.lse[((int64_t)b * p.H + h) * L + t];
+                // A row whose keys are all padded has LSE = -inf and no probabilities.
+                l2 = lse == -INFINITY ? INFINITY : lse * a.lmul;
+            }
+            lse2[row] = l2;
+            delta[row] = dl;
+        }
         return;
     }
     if constexpr (ROPE) {
-        // Rotate rows of Q_self (first half of items) and K_self (second half).
+        // Rotate rows of Q_self (first half of items) and K_self (second
+        // half); kRotItems<D> threads per row, each with an 8-dim chunk and
+        // its RoPE partner chunk (D = 24: one thread per row).
+        constexpr int H2 = D / 2, NPC = kRotItems<D>;
         const int64_t rows = (int64_t)p.B * p.H * Lp;
         int64_t item = (int64_t)(bid - nchain - nrow) * 256 + tid;
-        if (item >= 2 * rows) return;
-        const bool isk = item >= rows;
-        const int64_t row = isk ? item - rows : item;
+        if (item >= 2 * rows * NPC) return;
+        const bool isk = item >= rows * NPC;
+        if (isk) item -= rows * NPC;
+        const int64_t row = item / NPC;
+        const int pc = (int)(item % NPC);
         const int t = (int)(row % Lp);
         const int bh = (int)(row / Lp);
         const int b = bh / p.H, h = bh % p.H;
         const mpattn_tensor& src_t = isk ? p.k_self : p.q_self;
         const T* src = (const T*)src_t.ptr + b * src_t.stride_b + h * src_t.stride_h + (int64_t)t * src_t.stride_t;
         T* dst = (isk ? krot : qrot) + row * D;
+        if constexpr (H2 % 8 == 0) {
+            const int d0 = pc * 8;
+            float lo[8], hi[8];
+            if (t < L) {
+                float x[8], y[8];
+                load8f<T>(src, d0, x);
+                load8f<T>(src, d0 + H2, y);
+                const float* cr = p.rope_cos + (int64_t)t * H2 + d0;
+                const float* sr = p.rope_sin + (int64_t)t * H2 + d0;
 #pragma unroll
-        for (int d0 = 0; d0 < D; d0 += 8) {
-            float x[8];
-            if (t < L) load8_rot<T, D>(src, p.rope_cos, p.rope_sin, t, d0, 1.0f, true, x);
-            else
-                for (int u = 0; u < 8; ++u) x[u] = 0.f;
-            *reinterpret_cast<v8*>(dst + d0) = pack8<T>(x);
+                for (int u = 0; u < 8; ++u) {
+                    lo[u] = x[u] * cr[u] - y[u] * sr[u];
+                    hi[u] = y[u] * cr[u] + x[u] * sr[u];
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) lo[u] = hi[u] = 0.f;
+            }
+            *reinterpret_cast<v8*>(dst + d0) = pack8<T>(lo);
+            *reinterpret_cast<v8*>(dst + d0 + H2) = pack8<T>(hi);
+        } else {
+#pragma unroll
+            for (int d0 = 0; d0 < D; d0 += 8) {
+                float x[8];
+                if (t < L) load8_rot<T, D>(src, p.rope_cos, p.rope_sin, t, d0, 1.0f, true, x);
+                else
+                    for (int u = 0; u < 8; ++u) x[u] = 0.f;
+                *reinterpret_cast<v8*>(dst + d0) = pack8<T>(x);
+            }
         }
     }
 }
@@ -968,8 +1008,8 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     a.qrot = qrot;
     a.krot = krot;
     const int nchain = (p.B * (Lp / 64) + 3) / 4;
-    const int nrow = (int)(((int64_t)p.B * p.H * Lp + 255) / 256);
-    const int nrot = ROPE ? (int)((2 * (int64_t)p.B * p.H * Lp + 255) / 256) : 0;
+    const int nrow = (int)(((int64_t)p.B * p.H * Lp * kPrepLanes<D> + 255) / 256);
+    const int nrot = ROPE ? (int)((2 * (int64_t)p.B * p.H * Lp * kRotItems<D> + 255) / 256) : 0;
     hipLaunchKernelGGL((bwd_prep_kernel<T, D, ROPE, DENSE>), dim3(nchain + nrow + nrot), dim3(256), 0, stream,
                        a, lse2, delta, keff, ksum, qcid, qsum, qrot, krot, nchain, nrow);
     hipError_t e = hipGetLastError();
