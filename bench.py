@@ -151,12 +151,13 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--mode", choices=("fwd", "fwdbwd", "model", "attn3b", "attn650m", "combine"),
+    ap.add_argument("--mode", choices=("fwd", "fwdbwd", "model", "attn3b", "attn650m", "combine", "dense"),
                     default="fwd",
                     help="fwd: the headline forward (B=16); fwdbwd: forward + backward at the "
                          "training shape (B=8, dO ~ N(0, 1)); model: 650M MINT forward "
                          "sequences/s per attention path; attn3b / attn650m: the op at the 3B / "
-                         "650M model's attention shape; "
+                         "650M model's attention shape; dense: the 150M forward through the "
+                         "reference's (B, L, L) chain-mask contract; "
                          "combine: the materialised-logit combine fwd and bwd (HBM-bound)")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the 650M model forward summary of the default line")
@@ -199,6 +200,8 @@ def main():
         return bench_attn_shape(args, dev, args.mode[4:])
     if args.mode == "combine":
         return bench_combine(args, dev)
+    if args.mode == "dense":
+        return bench_dense(args, dev)
     xs, cid, pad = make_workload(dev)
     out = torch.empty_like(xs[0])
 
@@ -400,6 +403,35 @@ def bench_attn_shape(args, dev, shape):
         "config": {"workload": f"{name}-shape multi-pathway attention forward (one layer)",
                    "B": b, "H": h, "L": l, "D": d, "rope": "fused",
                    "chains": 3 if shape == "3b" else 2},
+        "kernel_ms": {"median": round(med, 5), "p10": round(per[len(per) // 10], 5),
+                      "p90": round(per[(9 * len(per)) // 10], 5)},
+        "pct_bf16_peak": round(100.0 * fl / (med * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+    }), flush=True)
+
+
+def bench_dense(args, dev):
+    """The 150M forward (the headline workload) with the chain information
+    given as the reference kernel's (B, L, L) bool mask (True = different
+    chains) instead of chain ids, fused RoPE."""
+    from mint_plus_amd import _lib
+    xs, cid, pad = make_workload(dev)
+    cm = (cid[:, :, None] != cid[:, None, :]).contiguous()
+    out = torch.empty_like(xs[0])
+
+    def step():
+        _lib.mpattn_fwd(*xs, chain_mask=cm, key_padding_mask=pad, rope=True, scale=D ** -0.5, out=out)
+
+    wall, per = timed(step, args.steps, args.warmup, torch.cuda.current_stream(dev))
+    med = statistics.median(per)
+    fl = flops_fwd()
+    print(json.dumps({
+        "metric": "multi-pathway attn fwd TFLOP/s (150M shape, dense chain mask, bf16)",
+        "value": round(fl / (med * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 5), "higher_is_better": True,
+        "dtype": "bf16", "data": "synthetic (the headline workload, mask from its chain ids)",
+        "config": {"workload": "150M isolated multi-pathway attention forward, (B, L, L) chain mask",
+                   "B": B, "H": H, "L": L, "D": D, "rope": "fused", "chains": 2},
         "kernel_ms": {"median": round(med, 5), "p10": round(per[len(per) // 10], 5),
                       "p90": round(per[(9 * len(per)) // 10], 5)},
         "pct_bf16_peak": round(100.0 * fl / (med * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),

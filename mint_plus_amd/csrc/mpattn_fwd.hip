@@ -87,6 +87,7 @@ struct FwdArgs {
     float qmul;    // factor applied to q while loading (scale*log2e when fused, else 1)
     float c;       // base-2 factor applied to raw logits (1 when fused)
     DropCfg drop;  // attention dropout (DROP kernels)
+    int mvec;      // dense mask rows readable as aligned 8-byte words
 };
 
 // ---------------------------------------------------------------------------
@@ -473,6 +474,30 @@ void fwd_kernel(const FwdArgs args) {
             mrow[u] = p.chain_mask + (int64_t)b * p.mask_stride_b +
                       (int64_t)(qvalid[u] ? qrow[u] : 0) * p.mask_stride_q;
     }
+    // Dense mask: each lane's mask bytes of a stage (8 keys per subtile half)
+    // are loaded one stage ahead, before the next copy is issued, and land
+    // by the compiler-visible wait at the top of the stage that reads them.
+    constexpr bool DMP = DENSE && NBUF == 2;
+    uint64_t mcur[QB][2][2], mnxt[QB][2][2];
+    auto mload = [&](int s, uint64_t (*m)[2][2]) {
+#pragma unroll
+        for (int u = 0; u < QB; ++u)
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int cc = 0; cc < 2; ++cc) {
+                    const int kg = s * kBN + st * 32 + 16 * cc + 8 * hh;
+                    uint64_t w = 0;
+                    if (args.mvec && kg + 8 <= L) {
+                        w = *reinterpret_cast<const uint64_t*>(mrow[u] + kg);
+                    } else {
+                        for (int t = 0; t < 8; ++t)
+                            if (kg + t < L && mrow[u][(int64_t)(kg + t) * p.mask_stride_k] != 0)
+                                w |= 0xffull << (8 * t);
+                    }
+                    m[u][st][cc] = w;
+                }
+    };
 
     // ---- softmax state, per query block ----
     // Probabilities are exp2(s2 - m_ref) with s2 = c * s the base-2 logit.
@@ -713,7 +738,11 @@ void fwd_kernel(const FwdArgs args) {
                 const i32x4 c0 = *reinterpret_cast<const i32x4*>(&cid[kl]);
                 const i32x4 c1 = *reinterpret_cast<const i32x4*>(&cid[kl + 4]);
                 uint32_t mbits = 0;
-                if constexpr (DENSE) {
+                if constexpr (DMP) {
+                    const uint64_t mw = st ? mcur[u][1][cc] : mcur[u][0][cc];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) mbits |= (uint32_t)(((mw >> (8 * t)) & 0xffu) != 0) << t;
+                } else if constexpr (DENSE) {
                     const int kg = k0 + kl;
                     for (int t = 0; t < 8; ++t)
                         if (kg + t < L)
@@ -901,6 +930,7 @@ void fwd_kernel(const FwdArgs args) {
     };
 
     // ---- main loop over stages ----
+    if constexpr (DMP) mload(0, mcur);
     build_ctrl(0);
     // Every prologue load (Q, chain ids, summaries) and the stage-0 copy have
     // landed here. The compiler sees this wait (the copies are inline asm it
@@ -918,7 +948,8 @@ void fwd_kernel(const FwdArgs args) {
         int allow = 0;  // copies of later stages that may stay in flight
 #pragma unroll
         for (int k = 1; k < NBUF - 1; ++k) allow += pend[k];
-        wait_vm_var(allow);
+        if constexpr (DMP) __builtin_amdgcn_s_waitcnt(0x0F70);  // (allow == 0) the mask words too
+        else wait_vm_var(allow);
         stage_barrier();
 #pragma unroll
         for (int k = 0; k < NBUF - 1; ++k) pend[k] = pend[k + 1];
@@ -931,6 +962,8 @@ void fwd_kernel(const FwdArgs args) {
             c0[u] = (cw >> (6 * u)) & 7;
             c1[u] = (cw >> (6 * u + 3)) & 7;
         }
+        if constexpr (DMP)
+            if (s + 1 < nst) mload(s + 1, mnxt);
         if (s + NBUF - 1 < nst) {
             const int bn = bf + NBUF - 1 >= NBUF ? bf - 1 : bf + NBUF - 1;
             pend[NBUF - 2] = issue(s + NBUF - 1, bn);
@@ -972,6 +1005,14 @@ void fwd_kernel(const FwdArgs args) {
             });
         }
         bf = bf + 1 == NBUF ? 0 : bf + 1;
+        if constexpr (DMP) {
+#pragma unroll
+            for (int u = 0; u < QB; ++u)
+#pragma unroll
+                for (int st = 0; st < 2; ++st)
+#pragma unroll
+                    for (int cc = 0; cc < 2; ++cc) mcur[u][st][cc] = mnxt[u][st][cc];
+        }
     }
 
     // ---- epilogue: normalise, store O and LSE ----
@@ -1093,6 +1134,8 @@ hipError_t launch_fwd16(const mpattn_fwd_params& p, hipStream_t stream) {
     a.qmul = fused ? f : 1.0f;
     a.c = fused ? 1.0f : f;
     a.drop = drop_cfg(p.dropout_p, p.dropout_seed);
+    a.mvec = p.chain_mask && p.mask_stride_k == 1 && (uintptr_t)p.chain_mask % 8 == 0 && p.mask_stride_b % 8 == 0 &&
+             p.mask_stride_q % 8 == 0;
     if (p.dtype == MPATTN_BF16) return dispatch_fwd_t<bf16_t>(a, stream);
     return dispatch_fwd_t<fp16_t>(a, stream);
 }
