@@ -89,6 +89,7 @@ struct BwdArgs {
     float c;     // logit factor: scale * log2(e), halved for sqrt-softmax
     float lmul;  // LSE factor: log2(e), halved for sqrt-softmax
     DropCfg drop;
+    int mvec;  // dense mask rows readable as aligned 8-byte words
 };
 
 // ---------------------------------------------------------------------------
@@ -851,6 +852,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     };
 
     // One 32-key subtile; mode 0/1: pure pathway, 2: both pathways.
+    uint64_t mcur[2][2], mnxt[2][2];  // dense mask words (see mload below)
     auto subtile = [&](const char* stage, const int* cid, int st, int mode, int k0) {
         f32x16 dsv;
         bool same[16];
@@ -894,8 +896,9 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
                     const int i = 8 * cc + t;
                     bool sm_;
                     if constexpr (DENSE) {
-                        const int kg = k0 + kl + t;
-                        sm_ = !(kg < L && mrow[(int64_t)kg * p.mask_stride_k] != 0);
+                        // mask word prefetched one stage ahead (key kl + t)
+                        const uint64_t mw = st ? mcur[1][cc] : mcur[0][cc];
+                        sm_ = ((mw >> (8 * t)) & 0xffu) == 0;
                     } else {
                         sm_ = ck == cq;
                     }
@@ -936,6 +939,26 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     };
 
     const int nst = (L + kBS - 1) / kBS;
+    // Dense mask: each lane's mask bytes of a stage (8 keys per subtile half,
+    // keys past L read as 0) are loaded one stage ahead, before the next copy
+    // is issued, and land by the compiler-visible wait at the stage top.
+    auto mload = [&](int s, uint64_t (*m)[2]) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                const int kg = s * kBS + st * 32 + 16 * cc + 8 * hh;
+                uint64_t w = 0;
+                if (a.mvec && kg + 8 <= L) {
+                    w = *reinterpret_cast<const uint64_t*>(mrow + kg);
+                } else {
+                    for (int t = 0; t < 8; ++t)
+                        if (kg + t < L && mrow[(int64_t)(kg + t) * p.mask_stride_k] != 0) w |= 0xffull << (8 * t);
+                }
+                m[st][cc] = w;
+            }
+    };
+    if constexpr (DENSE) mload(0, mcur);
     // Key summaries of a window of 64 subtiles (32 stages), one per lane,
     // read with readlane (as in the dK/dV kernel).
     auto sum_window = [&](int first) {
@@ -955,6 +978,8 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
             ksw = sum_window(sub0);
             __builtin_amdgcn_s_waitcnt(0x0F70);  // before the next copy is issued
         }
+        if constexpr (DENSE)
+            if (s + 1 < nst) mload(s + 1, mnxt);
         if (s + 1 < nst) issue(s + 1, bf ^ 1);
         const char* stage = smem + bf * STAGE;
         const int* cid = &scid[wave][bf][0];
@@ -967,6 +992,12 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
             if (md == 0) subtile(stage, cid, st, 0, k0);
             else if (md == 1) subtile(stage, cid, st, 1, k0);
             else if (md == 2) subtile(stage, cid, st, 2, k0);
+        }
+        if constexpr (DENSE) {
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int cc = 0; cc < 2; ++cc) mcur[st][cc] = mnxt[st][cc];
         }
     }
     wait_vm<0>();
@@ -989,6 +1020,8 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     a.c = p.scale * kLog2e * (SQRT ? 0.5f : 1.0f);
     a.lmul = kLog2e * (SQRT ? 0.5f : 1.0f);
     a.drop = drop_cfg(p.dropout_p, p.dropout_seed);
+    a.mvec = p.chain_mask && p.mask_stride_k == 1 && (uintptr_t)p.chain_mask % 8 == 0 && p.mask_stride_b % 8 == 0 &&
+             p.mask_stride_q % 8 == 0;
     const BwdWs ws = bwd_ws_layout(p.B, p.H, p.L, D, sizeof(T), ROPE);
     char* w = (char*)p.workspace;
     float* lse2 = (float*)(w + ws.lse2);
