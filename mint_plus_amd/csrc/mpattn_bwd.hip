@@ -90,6 +90,7 @@ struct BwdArgs {
     float lmul;  // LSE factor: log2(e), halved for sqrt-softmax
     DropCfg drop;
     int mvec;  // dense mask rows readable as aligned 8-byte words
+    int mdma;  // dense mask tiles copyable to LDS in 16-byte chunks (dK/dV)
 };
 
 // ---------------------------------------------------------------------------
@@ -321,8 +322,13 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     constexpr int TOT = NTEN * TS::NI;
     constexpr int NJ = (TOT + W - 1) / W;  // copies per wave (the last may be idle)
     constexpr int AUX = 4 * kBS * 4;  // lse2, delta, qcid (+ spare) floats/ints
-    constexpr int STAGE = NTEN * TS::TILE + AUX;
+    // Dense mask: the stage's tile of mask bytes, kBS query rows x the
+    // workgroup's 32 W keys, copied with the stage (when a.mdma).
+    constexpr int MROW = 32 * W;
+    constexpr int MSK = DENSE ? kBS * MROW : 0;
+    constexpr int STAGE = NTEN * TS::TILE + AUX + MSK;
     constexpr int NBUF = 2;
+    static_assert(!DENSE || (kBS * MROW) % (1024 * W) == 0, "mask tile copies split evenly over the waves");
     const mpattn_bwd_params& p = a.p;
 
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE > W * 32 * 65 * 4 ? NBUF * STAGE
@@ -360,6 +366,17 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     // ---- key-side registers: B operands K[key][dims kk*16 + 8*hh + (0..7)] ----
     v8 kf[2][BS::NKK], vf[2][BS::NKK];
     const bool kin = key < L;
+    // Dense mask tile: the workgroup's first key, and this lane's byte
+    // offset in a tile row. The last 16-key chunk that holds keys < L is
+    // copied from L - 16 (never past a row), so its bytes sit shifted.
+    const int mkb0 = kblk * MROW;
+    int mkoff = key - mkb0;
+    {
+        const int rem = L - mkb0;
+        if (rem < MROW && rem % 16 != 0 && mkoff / 16 == rem / 16) mkoff += 16 - rem % 16;
+        if (!kin) mkoff = 0;
+    }
+    const uint8_t* const mask_b = DENSE ? p.chain_mask + (int64_t)b * p.mask_stride_b : nullptr;
 #pragma unroll
     for (int kk = 0; kk < BS::NKK; ++kk) {
         const int d0 = kk * 16 + hh * 8;
@@ -436,6 +453,19 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
         for (int j = 0; j < NJ; ++j)
             if (TOT % W == 0 || wave + j * W < TOT) dma16(dsb[j], voff[j], lb + dlds[j]);
         dma4(aux_src, (unsigned)(q0 + lane) * 4u, lb + NTEN * TS::TILE + aux * kBS * 4);
+        if constexpr (DENSE) {
+            if (a.mdma) {
+                // Copy m: tile rows 8m .. 8m+7, 16-byte chunk lane % 8 of each
+                // (rows past L read row L-1; chunks past L read from L - 16).
+#pragma unroll
+                for (int m = wave; m < MSK / 1024; m += W) {
+                    const int row = min(q0 + m * 8 + (lane >> 3), L - 1);
+                    const int cst = min(mkb0 + (lane & 7) * 16, L - 16);
+                    dma16(mask_b, (unsigned)((int64_t)row * p.mask_stride_q + cst),
+                          lb + NTEN * TS::TILE + AUX + m * 1024);
+                }
+            }
+        }
         m0_restore(m0v);
     };
 
@@ -563,10 +593,16 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
             for (int i = 0; i < 16; ++i) {
                 bool sm_;
                 if constexpr (DENSE) {
-                    const int qg = q0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8);
-                    sm_ = !(qg < L && kin &&
-                            p.chain_mask[(int64_t)b * p.mask_stride_b + (int64_t)qg * p.mask_stride_q +
-                                         (int64_t)key * p.mask_stride_k] != 0);
+                    const int ql_ = st * 32 + 16 * (i / 8) + 8 * hh + (i % 8);
+                    const int qg = q0 + ql_;
+                    bool mb;
+                    if (a.mdma) {
+                        mb = *(reinterpret_cast<const uint8_t*>(stage + NTEN * TS::TILE + AUX) + ql_ * MROW + mkoff) != 0;
+                    } else {
+                        mb = p.chain_mask[(int64_t)b * p.mask_stride_b + (int64_t)qg * p.mask_stride_q +
+                                          (int64_t)key * p.mask_stride_k] != 0;
+                    }
+                    sm_ = !(qg < L && kin && mb);
                 } else {
                     sm_ = qc[i] == ckey;
                 }
@@ -1022,6 +1058,8 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     a.drop = drop_cfg(p.dropout_p, p.dropout_seed);
     a.mvec = p.chain_mask && p.mask_stride_k == 1 && (uintptr_t)p.chain_mask % 8 == 0 && p.mask_stride_b % 8 == 0 &&
              p.mask_stride_q % 8 == 0;
+    a.mdma = p.chain_mask && p.mask_stride_k == 1 && (uintptr_t)p.chain_mask % 16 == 0 && p.mask_stride_b % 16 == 0 &&
+             p.mask_stride_q % 16 == 0 && p.L >= 16 && (int64_t)p.L * p.mask_stride_q < ((int64_t)1 << 31);
     const BwdWs ws = bwd_ws_layout(p.B, p.H, p.L, D, sizeof(T), ROPE);
     char* w = (char*)p.workspace;
     float* lse2 = (float*)(w + ws.lse2);
