@@ -56,8 +56,9 @@ inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 //                               1 if the padded keys are a suffix of the 32
 //   qsum int32 [B][Lp/32][4]    queries: min chain, max chain (queries < L), 0, 0
 //   krot T     [B][H][Lp][D]    RoPE-rotated K_self (fused RoPE only)
+//   mcode u8   [B][Lp/32][Lp/32] dense mask: code of each 32 x 32 block
 struct FwdWs {
-    int64_t keff, ksum, qsum, krot, total;
+    int64_t keff, ksum, qsum, krot, mcode, total;
 };
 
 inline FwdWs fwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
@@ -68,7 +69,8 @@ inline FwdWs fwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
     w.ksum = al(w.keff + (int64_t)B * Lp * 4);
     w.qsum = al(w.ksum + (int64_t)B * (Lp / 32) * 16);
     w.krot = al(w.qsum + (int64_t)B * (Lp / 32) * 16);
-    w.total = al(w.krot + (rope ? (int64_t)B * H * Lp * D * esize : 0));
+    w.mcode = al(w.krot + (rope ? (int64_t)B * H * Lp * D * esize : 0));
+    w.total = al(w.mcode + (int64_t)B * (Lp / 32) * (Lp / 32));
     return w;
 }
 
@@ -87,6 +89,7 @@ struct FwdArgs {
     float qmul;    // factor applied to q while loading (scale*log2e when fused, else 1)
     float c;       // base-2 factor applied to raw logits (1 when fused)
     DropCfg drop;  // attention dropout (DROP kernels)
+    const uint8_t* mcode;  // dense mask block codes (0 all same chain, 1 all different, 2 mixed)
     int mvec;      // dense mask rows readable as aligned 8-byte words
 };
 
@@ -95,9 +98,49 @@ struct FwdArgs {
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool ROPE, bool DENSE>
 __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p, int* keff,
-                                                       int* ksum, int* qsum, T* krot, int Lp, int nchain) {
+                                                       int* ksum, int* qsum, T* krot, int Lp, int nchain,
+                                                       uint8_t* mcode, int64_t nrot) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int L = p.L;
+    if constexpr (DENSE) {
+        if ((int64_t)blockIdx.x >= nchain + nrot) {
+            // Dense mask: one wave per 32 x 32 block (lane: query row lane/2,
+            // 16 keys), code 0 if every entry with query and key < L is 0
+            // (same chain), 1 if every one is nonzero, 2 if mixed.
+            const int nb = Lp / 32;
+            const int64_t blk = ((int64_t)blockIdx.x - nchain - nrot) * 4 + wave;
+            if (blk >= (int64_t)p.B * nb * nb) return;
+            const int b = (int)(blk / ((int64_t)nb * nb));
+            const int rem = (int)(blk % ((int64_t)nb * nb));
+            const int q = (rem / nb) * 32 + (lane >> 1), k0 = (rem % nb) * 32 + (lane & 1) * 16;
+            bool any1 = false, any0 = false;
+            if (q < L) {
+                const uint8_t* row = p.chain_mask + (int64_t)b * p.mask_stride_b + (int64_t)q * p.mask_stride_q;
+                const bool vec = p.mask_stride_k == 1 && ((uintptr_t)p.chain_mask & 7) == 0 &&
+                                 (p.mask_stride_b & 7) == 0 && (p.mask_stride_q & 7) == 0;
+                if (vec && k0 + 16 <= L) {
+                    const uint64_t w0 = *reinterpret_cast<const uint64_t*>(row + k0);
+                    const uint64_t w1 = *reinterpret_cast<const uint64_t*>(row + k0 + 8);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        const bool v0 = ((w0 >> (8 * t)) & 0xff) != 0, v1 = ((w1 >> (8 * t)) & 0xff) != 0;
+                        any1 = any1 || v0 || v1;
+                        any0 = any0 || !v0 || !v1;
+                    }
+                } else {
+                    for (int t = 0; t < 16; ++t)
+                        if (k0 + t < L) {
+                            const bool v = row[(int64_t)(k0 + t) * p.mask_stride_k] != 0;
+                            any1 = any1 || v;
+                            any0 = any0 || !v;
+                        }
+                }
+            }
+            const bool a1 = __builtin_amdgcn_ballot_w64(any1) != 0, a0 = __builtin_amdgcn_ballot_w64(any0) != 0;
+            if (lane == 0) mcode[blk] = a1 ? (a0 ? 2 : 1) : 0;
+            return;
+        }
+    }
     if ((int)blockIdx.x < nchain) {
         const int ngrp = Lp / 64;
         const int gid = blockIdx.x * 4 + wave;
@@ -897,10 +940,26 @@ void fwd_kernel(const FwdArgs args) {
         if (kb < Lp / 32) sm = ksum_b[kb];
         return sm;
     };
-    auto set_codes = [&](const int4 sm) {
+    // Dense mask: the block code of (this block's 32 queries, subtile kbi)
+    // from the prep kernel decides the path like the chain summaries do.
+    auto dense_mode = [&](const int4 sm, int mc) -> int {
+        if (sm.z == 32) return 4;
+        if (mc == 2) return 3;
+        if (sm.z == 0) return mc ? 1 : 0;
+        if (sm.w) return mc ? 6 : 5;
+        return 3;
+    };
+    auto set_codes = [&](const int4 sm, int kbi) {
 #pragma unroll
         for (int u = 0; u < QB; ++u) {
-            const int code = subtile_mode(sm.x, sm.y, sm.z, sm.w, cq_min[u], cq_max[u]);
+            int code;
+            if constexpr (DENSE) {
+                const int nb = Lp / 32, qbk = (qv0 >> 5) + u;
+                const int mc = kbi < nb ? args.mcode[((int64_t)b * nb + (qbk < nb ? qbk : 0)) * nb + kbi] : 2;
+                code = dense_mode(sm, mc);
+            } else {
+                code = subtile_mode(sm.x, sm.y, sm.z, sm.w, cq_min[u], cq_max[u]);
+            }
             mb0[u] = __builtin_amdgcn_ballot_w64(code & 1);
             mb1[u] = __builtin_amdgcn_ballot_w64((code >> 1) & 1);
             mb2[u] = __builtin_amdgcn_ballot_w64((code >> 2) & 1);
@@ -915,7 +974,7 @@ void fwd_kernel(const FwdArgs args) {
     auto build_ctrl = [&](int s0) {
         sw0 = s0;
         const int4 sm = ksum_at(2 * s0);  // lane: subtile 2*s0 + lane
-        set_codes(sm);
+        set_codes(sm, 2 * s0 + lane);
         const int t2 = 2 * (lane & 31);
         int w = 0;
 #pragma unroll
@@ -1063,8 +1122,11 @@ static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     const int nchain = (p.B * (Lp / 64) + 3) / 4;
     constexpr int NPC = ((D / 2) % 8 == 0) ? D / 16 : 1;
     const int64_t nrot = ROPE ? ((int64_t)p.B * p.H * Lp * NPC + 255) / 256 : 0;
-    hipLaunchKernelGGL((fwd_prep_kernel<T, D, ROPE, DENSE>), dim3((unsigned)(nchain + nrot)), dim3(256), 0,
-                       stream, p, keff, ksum, qsum, krot, Lp, nchain);
+    uint8_t* mcode = (uint8_t*)(wsb + ws.mcode);
+    a.mcode = mcode;
+    const int64_t nmc = DENSE ? ((int64_t)p.B * (Lp / 32) * (Lp / 32) + 3) / 4 : 0;
+    hipLaunchKernelGGL((fwd_prep_kernel<T, D, ROPE, DENSE>), dim3((unsigned)(nchain + nrot + nmc)), dim3(256), 0,
+                       stream, p, keff, ksum, qsum, krot, Lp, nchain, mcode, nrot);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nqb = (p.L + 32 * C::QB * C::W - 1) / (32 * C::QB * C::W);
@@ -1089,10 +1151,10 @@ hipError_t launch_fwd_prep_f32(const mpattn_fwd_params& p, int* keff, int* ksum,
     const int nchain = (p.B * (Lp / 64) + 3) / 4;
     if (p.chain_mask)
         hipLaunchKernelGGL((fwd_prep_kernel<float, 16, false, true>), dim3((unsigned)nchain), dim3(256), 0,
-                           stream, p, keff, ksum, qsum, (float*)nullptr, Lp, nchain);
+                           stream, p, keff, ksum, qsum, (float*)nullptr, Lp, nchain, (uint8_t*)nullptr, (int64_t)0);
     else
         hipLaunchKernelGGL((fwd_prep_kernel<float, 16, false, false>), dim3((unsigned)nchain), dim3(256), 0,
-                           stream, p, keff, ksum, qsum, (float*)nullptr, Lp, nchain);
+                           stream, p, keff, ksum, qsum, (float*)nullptr, Lp, nchain, (uint8_t*)nullptr, (int64_t)0);
     return hipGetLastError();
 }
 
