@@ -129,7 +129,8 @@ typedef struct mpattn_bwd_params {
  * dropout. The backward with the same seed regenerates the mask. */
 
 /* Workspace bytes mpattn_fwd needs (chain-id staging; RoPE-rotated K_self
- * when rope == MPATTN_ROPE_FUSED). */
+ * when rope == MPATTN_ROPE_FUSED; per-32x32-block codes of a dense chain
+ * mask, B * (L/32 rounded up to even)^2 bytes, reserved in every case). */
 int64_t mpattn_fwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D, int32_t dtype,
                                   int32_t rope);
 
