@@ -114,6 +114,28 @@ def test_bwd_no_rope_dense_mask(D):
     assert_grads(got, ref, f"dense D={D}")
 
 
+@pytest.mark.parametrize("L,Lpad,D", [(256, 256, 32), (200, 208, 32), (1000, 1008, 32), (136, 144, 64)])
+def test_bwd_dense_mask_tiles(L, Lpad, D):
+    """Dense masks whose rows are 16-byte aligned: dK/dV copies the mask
+    tiles into LDS. A padded row stride (Lpad > L) with L not a multiple of
+    16 exercises the last key chunk copied from L - 16."""
+    print(f"[bwd dense tiles] L={L} Lpad={Lpad} D={D}", flush=True)
+    m = _mpattn()
+    xs, go, cid, kp = make_inputs(2, 2, L, D, torch.bfloat16, seed=41 + L + D, nchains=3)
+    g = [x.to(DEV) for x in xs]
+    c = torch.from_numpy(cid)
+    full = torch.zeros(2, L, Lpad, dtype=torch.bool)
+    full[:, :, :L] = c[:, :, None] != c[:, None, :]
+    cm = full.to(DEV)[:, :, :L]
+    assert cm.stride(1) == Lpad
+    grads = m.fused_multi_pathway_attention_bwd(*g, cm, go.to(DEV), key_padding_mask=torch.from_numpy(kp).to(DEV),
+                                                rope=True, scale=D ** -0.5)
+    torch.cuda.synchronize()
+    got = [t.float().cpu().numpy().astype(np.float64) for t in grads]
+    ref = oracle_grads(xs, go, cid, kp, rope=True, scale=D ** -0.5)
+    assert_grads(got, ref, f"dense tiles L={L} Lpad={Lpad}")
+
+
 def test_bwd_fp16():
     print("[bwd fp16]", flush=True)
     xs, go, cid, kp = make_inputs(2, 3, 190, 32, torch.float16, seed=17)

@@ -128,6 +128,28 @@ def test_fwd_heavy_first_dispatch(B, H, L, D, nchains, dense):
     assert_close16(got, ref, f"dispatch B={B} H={H} L={L} dense={dense}")
 
 
+@pytest.mark.parametrize("L,Lpad,D,nchains", [(100, 100, 32, 3), (257, 257, 16, 2), (200, 208, 64, 3),
+                                              (384, 384, 32, 1)])
+def test_fwd_dense_mask_layouts(L, Lpad, D, nchains):
+    """Dense masks with rows that are not 8-byte aligned (odd L: byte loads
+    in the block classification and the per-stage mask words), a padded row
+    stride, and one chain (every mask block all-same: one-pathway paths)."""
+    print(f"[fwd dense layouts] L={L} Lpad={Lpad} D={D} chains={nchains}", flush=True)
+    m = _mpattn()
+    xs, cid, kp = make_inputs(2, 3, L, D, torch.bfloat16, seed=77 + L + D, nchains=nchains)
+    c = torch.from_numpy(cid)
+    full = torch.zeros(2, L, Lpad, dtype=torch.bool)
+    full[:, :, :L] = c[:, :, None] != c[:, None, :]
+    cm = full.to(DEV)[:, :, :L]
+    out = m.fused_multi_pathway_attention(*[x.to(DEV) for x in xs], cm, training=False,
+                                          key_padding_mask=torch.from_numpy(kp).to(DEV), rope=True,
+                                          scale=D ** -0.5)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy().astype(np.float64)
+    ref = oracle_out(xs, cid, kp, rope=True, scale=D ** -0.5)
+    assert_close16(got, ref, f"dense L={L} Lpad={Lpad} D={D}")
+
+
 def test_fwd_prerotated_contract():
     """Reference contract: q pre-scaled, q/k pre-rotated, scale 1, dense mask."""
     print("[fwd prerotated dense]", flush=True)
