@@ -1005,18 +1005,26 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     int sub0 = 0;
     int4 ksw = sum_window(0);
     issue(0, 0);
-    for (int s = 0; s < nst; ++s) {
+    // Key stages after the last one with a valid key (all padded) are not
+    // run; the first summary window decides (at least stage 0 runs).
+    int nrun = nst;
+    for (int s = 0; s < nrun; ++s) {
         const int bf = s & 1;
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), compiler-visible
         stage_barrier();
+        if (s == 0 && nst <= 32) {
+            const uint64_t live = __builtin_amdgcn_ballot_w64(ksw.z < 32) &
+                                  (nst >= 32 ? ~0ull : (1ull << (2 * nst)) - 1);
+            nrun = live ? (63 - __builtin_clzll(live)) / 2 + 1 : 1;
+        }
         if (2 * s - sub0 >= 64) {
             sub0 = 2 * s;
             ksw = sum_window(sub0);
             __builtin_amdgcn_s_waitcnt(0x0F70);  // before the next copy is issued
         }
         if constexpr (DENSE)
-            if (s + 1 < nst) mload(s + 1, mnxt);
-        if (s + 1 < nst) issue(s + 1, bf ^ 1);
+            if (s + 1 < nrun) mload(s + 1, mnxt);
+        if (s + 1 < nrun) issue(s + 1, bf ^ 1);
         const char* stage = smem + bf * STAGE;
         const int* cid = &scid[wave][bf][0];
         const int k0 = s * kBS;

@@ -996,14 +996,24 @@ void fwd_kernel(const FwdArgs args) {
     // cannot see), so it adds no vmcnt(0) at later uses, which would also
     // drain the copies in flight.
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // Stages after the last one with a valid key (every key padded: a skip
+    // for every wavefront, since it depends on the keys only) are not run.
+    // The first control window decides; longer sequences run every stage.
+    // At least stage 0 runs (its copy is in flight).
+    int nrun = nst;
+    if (nst <= 32) {
+        const uint64_t skip = mb2[0] & ~mb1[0] & ~mb0[0];  // code 4 per subtile (lane)
+        const uint64_t live = ~skip & (nst >= 32 ? ~0ull : (1ull << (2 * nst)) - 1);
+        nrun = live ? (63 - __builtin_clzll(live)) / 2 + 1 : 1;
+    }
     pend[0] = 0;
     // pend[k]: vector-memory instructions of stage s + k still in flight
     // (stage 0 was issued before the prologue and has landed).
 #pragma unroll
     for (int t = 1; t < NBUF - 1; ++t)
-        if (t < nst) pend[t] = issue(t, t);
+        if (t < nrun) pend[t] = issue(t, t);
     int bf = 0;
-    for (int s = 0; s < nst; ++s) {
+    for (int s = 0; s < nrun; ++s) {
         int allow = 0;  // copies of later stages that may stay in flight
 #pragma unroll
         for (int k = 1; k < NBUF - 1; ++k) allow += pend[k];
@@ -1022,8 +1032,8 @@ void fwd_kernel(const FwdArgs args) {
             c1[u] = (cw >> (6 * u + 3)) & 7;
         }
         if constexpr (DMP)
-            if (s + 1 < nst) mload(s + 1, mnxt);
-        if (s + NBUF - 1 < nst) {
+            if (s + 1 < nrun) mload(s + 1, mnxt);
+        if (s + NBUF - 1 < nrun) {
             const int bn = bf + NBUF - 1 >= NBUF ? bf - 1 : bf + NBUF - 1;
             pend[NBUF - 2] = issue(s + NBUF - 1, bn);
         }
