@@ -169,7 +169,7 @@ __device__ __forceinline__ void decode_bh(int bh, int H, int& b, int& h) {
 // ---------------------------------------------------------------------------
 // Forward (and the backward's statistics pass).
 // ---------------------------------------------------------------------------
-template <typename T, int ND, bool VEC, bool STATS>
+template <typename T, int ND, bool VEC, bool STATS, bool DROPK = true>
 __global__ __launch_bounds__(256) void combine_fwd_kernel(CombineArgs a) {
     constexpr int KC = 64;               // keys per LDS stage
     constexpr int DP = ND * 32;          // head dim padded to the MFMA tile
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(CombineArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[n][i] = 0.f;
     float mref = -INFINITY, lsum = 0.f;
-    const bool dropon = a.drop_on != 0;
+    const bool dropon = DROPK && a.drop_on != 0;
     const uint32_t drow = dropon ? drop_row(a.drop.lo, (uint32_t)bh, (uint32_t)q) : 0u;
 
     const int nch = D / 8;  // 8-element chunks per value row
@@ -661,10 +661,17 @@ template <typename T, int ND, bool VEC>
 hipError_t launch_combine_t(const CombineArgs& a, int mode, hipStream_t st) {
     const int nqb = (a.L + 127) / 128, nkb = (a.L + 63) / 64;
     const int bh = a.B * a.H;
+    // Without dropout the forward is instantiated with no dropout code.
     if (mode == 0) {
-        hipLaunchKernelGGL((combine_fwd_kernel<T, ND, VEC, false>), dim3(bh * nqb), dim3(256), 0, st, a);
+        if (a.drop_on)
+            hipLaunchKernelGGL((combine_fwd_kernel<T, ND, VEC, false, true>), dim3(bh * nqb), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((combine_fwd_kernel<T, ND, VEC, false, false>), dim3(bh * nqb), dim3(256), 0, st, a);
     } else {
-        hipLaunchKernelGGL((combine_fwd_kernel<T, ND, VEC, true>), dim3(bh * nqb), dim3(256), 0, st, a);
+        if (a.drop_on)
+            hipLaunchKernelGGL((combine_fwd_kernel<T, ND, VEC, true, true>), dim3(bh * nqb), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((combine_fwd_kernel<T, ND, VEC, true, false>), dim3(bh * nqb), dim3(256), 0, st, a);
         hipLaunchKernelGGL((combine_bwd_kernel<T, ND, VEC>), dim3(bh * nkb), dim3(256), 0, st, a);
     }
     return hipGetLastError();
