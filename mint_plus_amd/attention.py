@@ -114,14 +114,31 @@ class MultiHeadAttention(IncrementalStateMixin, nn.Module):
 
     def project_qkv(self, x: Tensor) -> Tensor:
         """(T, B, 3E) projection output [q | k | v], one GEMM. With separate
-        q/k/v projections the three weights are concatenated for the call."""
+        q/k/v projections the three weights are concatenated (see
+        ``_qkv_weight``)."""
         if self.use_fused_qkv:
             return self.fused_qkv(x)
-        w = torch.cat([self.q_proj.weight, self.k_proj.weight, self.v_proj.weight], 0)
-        b = None
-        if self.q_proj.bias is not None:
-            b = torch.cat([self.q_proj.bias, self.k_proj.bias, self.v_proj.bias], 0)
+        w, b = self._qkv_weight()
         return F.linear(x, w, b)
+
+    def _qkv_weight(self):
+        """[W_q; W_k; W_v] and the biases, concatenated. When a gradient is
+        recorded the concatenation is part of the call; otherwise it is kept
+        until a weight is replaced or modified in place (its storage or
+        version counter changes), so inference does not copy the weights on
+        every forward (at the cost of one extra copy held on the device)."""
+        ps = [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight]
+        bs = [self.q_proj.bias, self.k_proj.bias, self.v_proj.bias]
+        has_b = bs[0] is not None
+        tensors = ps + (bs if has_b else [])
+        if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+            return torch.cat(ps, 0), (torch.cat(bs, 0) if has_b else None)
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in tensors)
+        cache = getattr(self, "_qkv_cache", None)
+        if cache is None or cache[0] != key:
+            cache = (key, torch.cat(ps, 0), torch.cat(bs, 0) if has_b else None)
+            self._qkv_cache = cache
+        return cache[1], cache[2]
 
     def project_qkv_4d(self, x: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
         """q, k, v as contiguous (B, H, T, D); scale and RoPE are left to the

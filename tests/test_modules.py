@@ -161,3 +161,28 @@ def test_hip_paths_have_no_cpu_fallback():
         with pytest.raises((RuntimeError, AssertionError, ValueError, TypeError)):
             with torch.no_grad():
                 layer(x, chain_ids=cid)
+
+
+def test_project_qkv_weight_cache():
+    """project_qkv with separate q/k/v projections: in inference the
+    concatenated weight is reused across calls and rebuilt after an in-place
+    update; with gradients the concatenation stays in the graph."""
+    from mint_plus_amd.attention import MultiHeadAttention
+    torch.manual_seed(5)
+    mha = MultiHeadAttention(16, 2)
+    x = torch.randn(5, 3, 16)
+    ref = torch.cat([mha.q_proj(x), mha.k_proj(x), mha.v_proj(x)], -1)
+    with torch.no_grad():
+        a = mha.project_qkv(x)
+        w_first = mha._qkv_cache[1]
+        b = mha.project_qkv(x)
+        assert mha._qkv_cache[1] is w_first
+        torch.testing.assert_close(a, ref.detach())
+        torch.testing.assert_close(b, ref.detach())
+        mha.k_proj.weight.add_(0.5)
+        c = mha.project_qkv(x)
+        assert mha._qkv_cache[1] is not w_first
+        torch.testing.assert_close(c[..., 16:32], mha.k_proj(x))
+    out = mha.project_qkv(x)
+    out.sum().backward()
+    assert mha.q_proj.weight.grad is not None and mha.v_proj.bias.grad is not None
