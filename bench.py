@@ -67,11 +67,31 @@ def bytes_bwd(b=B):
     return 14.0 * b * H * L * D * 2 + b * H * L * 4 + b * L * 5
 
 
+def host_cores():
+    """(threads, CPU model): every core this process may run on
+    (sched_getaffinity), capped by OMP_NUM_THREADS when the host sets it (the
+    GPU box's CPU share), and the model name from /proc/cpuinfo."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return n, model
+
+
 def cpu_baseline(budget_s=20.0):
     """fp32 eager restatement (oracle/torch_ref.py) on host cores, one batch
     element at a time, until ~budget_s of CPU work; reported as TFLOP/s."""
     from oracle import torch_ref
-    threads = min(os.cpu_count() or 1, 16)
+    threads, cpu = host_cores()
     torch.set_num_threads(threads)
     torch.set_float32_matmul_precision("highest")
     xs, cid, pad = make_workload("cpu")
@@ -91,9 +111,11 @@ def cpu_baseline(budget_s=20.0):
         b += 1
     med = statistics.median(times)
     return {"value": per_elem / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu,
             "sample": f"fp32 eager restatement (oracle/torch_ref.py), {len(times)} of {B} batch "
                       f"elements of the 150M shape timed one at a time, median "
-                      f"{med * 1e3:.1f} ms/element (full batch ~{med * B:.2f} s)"}
+                      f"{med * 1e3:.1f} ms/element (full batch ~{med * B:.2f} s), "
+                      f"{threads} threads on {cpu}"}
 
 
 def model_batch(device, seed, B, lo, hi, min_chain):

@@ -34,7 +34,11 @@
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
  *   - All tensors are 4-D (B, H, L, D) views given by a base pointer and
  *     element strides for b, h and t; the head-dim stride must be 1.
- *     This admits the (L, B, 3E) projection output without a copy.
+ *     This admits the (L, B, 3E) projection output without a copy. Rows
+ *     start 16-byte aligned, and the kernels address rows with 32-bit byte
+ *     offsets from each (b, h) base: L * stride_t * element size must stay
+ *     below 2^31 (likewise L * mask_stride_q for a dense chain mask in the
+ *     backward). Larger requests return MPATTN_ERR_UNSUPPORTED.
  *   - Return 0 on success, a negative MPATTN_ERR_* code on error. Arguments
  *     are validated before anything is enqueued.
  */
@@ -47,7 +51,7 @@
 extern "C" {
 #endif
 
-#define MPATTN_VERSION 3
+#define MPATTN_VERSION 4
 
 enum {
     MPATTN_OK = 0,
@@ -92,7 +96,7 @@ typedef struct mpattn_fwd_params {
     int32_t sqrt_softmax;    /* 1: O = sum sqrt(P) V (muS variant)           */
     float dropout_p;         /* attention dropout in [0, 1); > 0 needs 16-bit
                                 inputs and sqrt_softmax == 0               */
-    void *workspace;         /* >= mpattn_fwd_workspace_size() bytes, 16-byte
+    void *workspace;         /* >= mpattn_fwd_workspace_size() bytes, 256-byte
                                 aligned; contents need no initialisation   */
     int64_t workspace_bytes;
     uint64_t dropout_seed;   /* seed of the dropout mask (see below)         */
@@ -109,7 +113,9 @@ typedef struct mpattn_bwd_params {
     int64_t mask_stride_b, mask_stride_q, mask_stride_k;
     const uint8_t *key_pad;
     const float *rope_cos, *rope_sin;
-    void *workspace;          /* >= mpattn_bwd_workspace_size() bytes       */
+    void *workspace;          /* >= mpattn_bwd_workspace_size() bytes, 16-byte
+                                 aligned; contents need no initialisation  */
+    int64_t workspace_bytes;  /* size of the buffer at workspace            */
     int32_t B, H, L, D;
     int32_t dtype, rope;
     float scale;
@@ -173,6 +179,7 @@ typedef struct mpattn_combine_bwd_params {
     int64_t mask_stride_b, mask_stride_q, mask_stride_k;
     void *workspace;         /* >= mpattn_combine_bwd_workspace_size() bytes,
                                 256-byte aligned                            */
+    int64_t workspace_bytes; /* size of the buffer at workspace             */
     int32_t B, H, L, D;
     int32_t dtype;
     float dropout_p;         /* the forward's dropout_p and dropout_seed    */

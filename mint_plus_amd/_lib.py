@@ -78,7 +78,7 @@ class BwdParams(ctypes.Structure):
         ("mask_stride_k", ctypes.c_int64),
         ("key_pad", ctypes.c_void_p),
         ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p),
-        ("workspace", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
         ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("L", ctypes.c_int32), ("D", ctypes.c_int32),
         ("dtype", ctypes.c_int32), ("rope", ctypes.c_int32),
         ("scale", ctypes.c_float), ("sqrt_softmax", ctypes.c_int32),
@@ -111,7 +111,7 @@ class CombineBwdParams(ctypes.Structure):
         ("chain_mask", ctypes.c_void_p),
         ("mask_stride_b", ctypes.c_int64), ("mask_stride_q", ctypes.c_int64),
         ("mask_stride_k", ctypes.c_int64),
-        ("workspace", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
         ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("L", ctypes.c_int32), ("D", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
         ("dropout_p", ctypes.c_float), ("dropout_seed", ctypes.c_uint64),
@@ -188,25 +188,30 @@ _rope_lock = threading.Lock()
 
 
 def rope_tables(L, D, device):
-    """Cached device cos/sin tables (L, D/2) fp32 of ``t * inv_freq``.
+    """Device cos/sin tables (L, D/2) fp32 of ``t * inv_freq``.
 
     ``inv_freq = 1 / 10000**(arange(0, D, 2) / D)`` as in
     mint_plus/models/rotary_embedding.py:44, rounded to fp32; the angle is
     the fp32 product ``t * inv_freq`` (rotary_embedding.py:49-50); cos/sin are
     evaluated in fp64 on the host and rounded to fp32 once.
+
+    One table per (D, device) is kept, at the largest length seen so far
+    (rounded up to 256 rows); shorter lengths get its first L rows (rows are
+    indexed by position, so they are a prefix, and a contiguous view).
     """
     dev = torch.device(device)
-    key = (int(L), int(D), dev.type, dev.index)
+    key = (int(D), dev.type, dev.index)
     with _rope_lock:
         hit = _rope_cache.get(key)
-        if hit is not None:
-            return hit
-        inv = (1.0 / ROPE_BASE ** (np.arange(0, D, 2, dtype=np.float64) / D)).astype(np.float32)
-        ang = (np.arange(L, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float64)
-        cos = torch.from_numpy(np.cos(ang).astype(np.float32)).to(dev)
-        sin = torch.from_numpy(np.sin(ang).astype(np.float32)).to(dev)
-        _rope_cache[key] = (cos, sin)
-        return cos, sin
+        if hit is None or hit[0].shape[0] < L:
+            n = (int(L) + 255) // 256 * 256
+            inv = (1.0 / ROPE_BASE ** (np.arange(0, D, 2, dtype=np.float64) / D)).astype(np.float32)
+            ang = (np.arange(n, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float64)
+            cos = torch.from_numpy(np.cos(ang).astype(np.float32)).to(dev)
+            sin = torch.from_numpy(np.sin(ang).astype(np.float32)).to(dev)
+            hit = (cos, sin)
+            _rope_cache[key] = hit
+        return hit[0][:L], hit[1][:L]
 
 
 def _stream_handle(device):
@@ -280,7 +285,8 @@ def _aligned(t):
 
 def mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, *, chain_ids=None,
                chain_mask=None, key_padding_mask=None, rope=False, scale=1.0,
-               sqrt_softmax=False, dropout_p=0.0, dropout_seed=0, out=None, need_lse=False):
+               sqrt_softmax=False, dropout_p=0.0, dropout_seed=0, out=None, need_lse=False,
+               lse=None):
     """Launch the forward kernel on the current stream.
 
     Returns ``out`` (B, H, L, D) and, if ``need_lse``, the fp32 (B, H, L)
@@ -301,7 +307,13 @@ def mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, *, chain_ids=N
         out = torch.empty((B, H, L, D), dtype=q_self.dtype, device=dev)
     else:
         _check_out(out, (B, H, L, D), q_self, "out")
-    lse = torch.empty((B, H, L), dtype=torch.float32, device=dev) if need_lse else None
+    if need_lse and lse is None:
+        lse = torch.empty((B, H, L), dtype=torch.float32, device=dev)
+    elif need_lse and (tuple(lse.shape) != (B, H, L) or lse.dtype != torch.float32
+                       or not lse.is_contiguous() or lse.device != dev):
+        raise ValueError(f"lse must be a contiguous fp32 (B, H, L) = {(B, H, L)} tensor on {dev}")
+    elif not need_lse:
+        lse = None
     p = FwdParams()
     p.q_self, p.k_self, p.v_self, p.q_multi, p.k_multi, p.v_multi = (_t4(t) for t in ins)
     p.out = _t4(out)
@@ -373,7 +385,7 @@ def mpattn_bwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, out, lse, grad
     if rope:
         cos, sin = rope_tables(L, D, dev)
         p.rope_cos, p.rope_sin = cos.data_ptr(), sin.data_ptr()
-    p.workspace = ws.data_ptr()
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
     p.B, p.H, p.L, p.D = B, H, L, D
     p.dtype = _DTYPES[q_self.dtype]
     p.rope = MPATTN_ROPE_FUSED if rope else MPATTN_ROPE_NONE
@@ -468,7 +480,7 @@ def mpattn_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values, int
     p.d_intra_values, p.d_inter_values = _t4(d_vs), _t4(d_vm)
     p.chain_mask = cm.data_ptr()
     p.mask_stride_b, p.mask_stride_q, p.mask_stride_k = cm.stride()
-    p.workspace = ws.data_ptr()
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
     p.B, p.H, p.L, p.D = B, H, L, D
     p.dtype = _DTYPES[vs.dtype]
     p.dropout_p = float(dropout_p)

@@ -3,8 +3,10 @@
 ``MultiHeadAttention`` (attention.py:32-270) and ``MultimerAttention``
 (attention.py:273-371) keep the reference's constructor arguments, parameter
 names (so state dicts load unchanged), initialisation and methods. Both gain
-``project_qkv(x)``, which returns the (T, B, 3E) projection output that the
-fused multi-pathway op reads through strides (no head-major copies).
+``project_qkv(x)``, which returns the projection outputs in the (T, B, .)
+layout that the fused multi-pathway op reads through strides (no head-major
+copies): one (T, B, 3E) tensor for a fused projection, or q, k, v as three
+(T, B, E) tensors.
 
 The eager methods (``forward``, ``forward_before_softmax``) are torch
 compositions kept for the reference's non-fused paths; the multi-pathway
@@ -112,33 +114,14 @@ class MultiHeadAttention(IncrementalStateMixin, nn.Module):
             return tuple(t.contiguous() for t in self.fused_qkv(x).chunk(3, dim=-1))
         return self.q_proj(x), self.k_proj(x), self.v_proj(x)
 
-    def project_qkv(self, x: Tensor) -> Tensor:
-        """(T, B, 3E) projection output [q | k | v], one GEMM. With separate
-        q/k/v projections the three weights are concatenated (see
-        ``_qkv_weight``)."""
+    def project_qkv(self, x: Tensor):
+        """The projections in the (T, B, .) layout the fused kernels read by
+        strides: the (T, B, 3E) output [q | k | v] of the fused projection, or
+        the three (T, B, E) outputs q, k, v of separate projections (three
+        GEMMs; no weight concatenation, so nothing is cached across calls)."""
         if self.use_fused_qkv:
             return self.fused_qkv(x)
-        w, b = self._qkv_weight()
-        return F.linear(x, w, b)
-
-    def _qkv_weight(self):
-        """[W_q; W_k; W_v] and the biases, concatenated. When a gradient is
-        recorded the concatenation is part of the call; otherwise it is kept
-        until a weight is replaced or modified in place (its storage or
-        version counter changes), so inference does not copy the weights on
-        every forward (at the cost of one extra copy held on the device)."""
-        ps = [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight]
-        bs = [self.q_proj.bias, self.k_proj.bias, self.v_proj.bias]
-        has_b = bs[0] is not None
-        tensors = ps + (bs if has_b else [])
-        if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
-            return torch.cat(ps, 0), (torch.cat(bs, 0) if has_b else None)
-        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in tensors)
-        cache = getattr(self, "_qkv_cache", None)
-        if cache is None or cache[0] != key:
-            cache = (key, torch.cat(ps, 0), torch.cat(bs, 0) if has_b else None)
-            self._qkv_cache = cache
-        return cache[1], cache[2]
+        return self.q_proj(x), self.k_proj(x), self.v_proj(x)
 
     def project_qkv_4d(self, x: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
         """q, k, v as contiguous (B, H, T, D); scale and RoPE are left to the

@@ -50,6 +50,15 @@ int check_tensor(const mpattn_tensor& t, const char* name, int esize, bool out) 
     return MPATTN_OK;
 }
 
+// The kernels address rows with 32-bit byte offsets from each (b, h) base
+// (the DMA copies take a 32-bit per-lane offset); the last row's end must fit.
+int check_row_offsets(const mpattn_tensor* const* ts, const char* const* names, int n, int L, int esize) {
+    for (int i = 0; i < n; ++i)
+        if ((int64_t)L * ts[i]->stride_t * esize + 64 * esize > 0x7fffffffLL)
+            return fail(MPATTN_ERR_UNSUPPORTED, "%s: L * stride_t too large for 32-bit row offsets", names[i]);
+    return MPATTN_OK;
+}
+
 int check_common(int B, int H, int L, int D, int dtype, int rope, float scale,
                  const int32_t* chain_id, const uint8_t* chain_mask, int64_t msb, int64_t msq,
                  int64_t msk, const float* rc, const float* rs, int sqrt_softmax) {
@@ -105,7 +114,47 @@ int check_combine(int B, int H, int L, int D, int dtype, const uint8_t* mask, in
     return MPATTN_OK;
 }
 
+// Argument checks of mpattn_fwd / mpattn_fwd_noalloc (everything but the
+// workspace).
+int validate_fwd(const mpattn_fwd_params* p) {
+    if (!p) return fail(MPATTN_ERR_INVALID, "null params");
+    int rc = check_common(p->B, p->H, p->L, p->D, p->dtype, p->rope, p->scale, p->chain_id,
+                          p->chain_mask, p->mask_stride_b, p->mask_stride_q, p->mask_stride_k,
+                          p->rope_cos, p->rope_sin, p->sqrt_softmax);
+    if (rc) return rc;
+    if ((rc = check_dropout(p->dropout_p, p->dtype, p->sqrt_softmax))) return rc;
+    const int es = elt_size(p->dtype);
+    const mpattn_tensor* ts[7] = {&p->q_self, &p->k_self, &p->v_self, &p->q_multi,
+                                  &p->k_multi, &p->v_multi, &p->out};
+    const char* names[7] = {"q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi", "out"};
+    for (int i = 0; i < 7; ++i)
+        if ((rc = check_tensor(*ts[i], names[i], es, i == 6))) return rc;
+    if (p->lse && (uintptr_t)p->lse % 4) return fail(MPATTN_ERR_INVALID, "lse misaligned");
+    // Rows are addressed with 32-bit byte offsets from each (b, h) base.
+    if ((rc = check_row_offsets(ts, names, 6, p->L, es))) return rc;
+    return MPATTN_OK;
+}
+
+int launch_fwd_any(const mpattn_fwd_params& p, void* stream) {
+    hipError_t e;
+    if (p.dtype == MPATTN_FP32) {
+        e = mpattn::launch_fwd32(p, (hipStream_t)stream);
+    } else {
+        e = mpattn::launch_fwd16(p, (hipStream_t)stream);
+    }
+    if (e != hipSuccess) return fail(MPATTN_ERR_LAUNCH, "fwd launch: %s", hipGetErrorString(e));
+    return MPATTN_OK;
+}
+
 }  // namespace
+
+namespace mpattn {
+// Shared with the no-allocation entry point (mpattn_noalloc.hip).
+int api_validate_fwd(const mpattn_fwd_params* p) { return validate_fwd(p); }
+int api_launch_fwd(const mpattn_fwd_params& p, void* stream) { return launch_fwd_any(p, stream); }
+void api_clear_error() { g_last_error[0] = 0; }
+int api_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace mpattn
 
 extern "C" {
 
@@ -125,38 +174,15 @@ const char* mpattn_strerror(int code) {
 
 int mpattn_fwd(const mpattn_fwd_params* p, void* stream) {
     g_last_error[0] = 0;
-    if (!p) return fail(MPATTN_ERR_INVALID, "null params");
-    int rc = check_common(p->B, p->H, p->L, p->D, p->dtype, p->rope, p->scale, p->chain_id,
-                          p->chain_mask, p->mask_stride_b, p->mask_stride_q, p->mask_stride_k,
-                          p->rope_cos, p->rope_sin, p->sqrt_softmax);
+    int rc = validate_fwd(p);
     if (rc) return rc;
-    if ((rc = check_dropout(p->dropout_p, p->dtype, p->sqrt_softmax))) return rc;
-    const int es = elt_size(p->dtype);
-    const mpattn_tensor* ts[7] = {&p->q_self, &p->k_self, &p->v_self, &p->q_multi,
-                                  &p->k_multi, &p->v_multi, &p->out};
-    const char* names[7] = {"q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi", "out"};
-    for (int i = 0; i < 7; ++i)
-        if ((rc = check_tensor(*ts[i], names[i], es, i == 6))) return rc;
-    if (p->lse && (uintptr_t)p->lse % 4) return fail(MPATTN_ERR_INVALID, "lse misaligned");
-    // Rows are addressed with 32-bit byte offsets from each (b, h) base.
-    for (int i = 0; i < 6; ++i)
-        if ((int64_t)p->L * ts[i]->stride_t * es + 64 * es > 0x7fffffffLL)
-            return fail(MPATTN_ERR_UNSUPPORTED, "%s: L * stride_t too large for 32-bit row offsets",
-                        names[i]);
     {
         const int64_t need = mpattn::fwd_workspace_bytes(p->B, p->H, p->L, p->D, p->dtype, p->rope);
         if (!p->workspace || (uintptr_t)p->workspace % 256 || p->workspace_bytes < need)
             return fail(MPATTN_ERR_INVALID, "workspace: need %lld bytes, 256-byte aligned (got %lld)",
                         (long long)need, (long long)p->workspace_bytes);
     }
-    hipError_t e;
-    if (p->dtype == MPATTN_FP32) {
-        e = mpattn::launch_fwd32(*p, (hipStream_t)stream);
-    } else {
-        e = mpattn::launch_fwd16(*p, (hipStream_t)stream);
-    }
-    if (e != hipSuccess) return fail(MPATTN_ERR_LAUNCH, "fwd launch: %s", hipGetErrorString(e));
-    return MPATTN_OK;
+    return launch_fwd_any(*p, stream);
 }
 
 int64_t mpattn_fwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D, int32_t dtype,
@@ -188,8 +214,16 @@ int mpattn_bwd(const mpattn_bwd_params* p, void* stream) {
     for (int i = 0; i < 14; ++i)
         if ((rc = check_tensor(*ts[i], names[i], es, i >= 8))) return rc;
     if (!p->lse || (uintptr_t)p->lse % 4) return fail(MPATTN_ERR_INVALID, "lse required (fp32, aligned)");
-    if (!p->workspace || (uintptr_t)p->workspace % 16)
-        return fail(MPATTN_ERR_INVALID, "workspace required (16-byte aligned)");
+    if ((rc = check_row_offsets(ts, names, 14, p->L, es))) return rc;
+    if (p->chain_mask &&
+        (int64_t)p->L * p->mask_stride_q + (int64_t)p->L * p->mask_stride_k + 16 > 0x7fffffffLL)
+        return fail(MPATTN_ERR_UNSUPPORTED, "chain_mask: L * mask_stride_q too large for 32-bit row offsets");
+    {
+        const int64_t need = mpattn::bwd_workspace_bytes(p->B, p->H, p->L, p->D);
+        if (!p->workspace || (uintptr_t)p->workspace % 16 || p->workspace_bytes < need)
+            return fail(MPATTN_ERR_INVALID, "workspace: need %lld bytes, 16-byte aligned (got %lld)",
+                        (long long)need, (long long)p->workspace_bytes);
+    }
     hipError_t e = mpattn::launch_bwd(*p, (hipStream_t)stream);
     if (e == hipErrorInvalidValue) return fail(MPATTN_ERR_UNSUPPORTED, "bwd: configuration not built");
     if (e != hipSuccess) return fail(MPATTN_ERR_LAUNCH, "bwd launch: %s", hipGetErrorString(e));
@@ -242,8 +276,12 @@ int mpattn_combine_bwd(const mpattn_combine_bwd_params* p, void* stream) {
     for (int i = 0; i < 4; ++i)
         if (!lt[i]->ptr || lt[i]->stride_b < 0 || lt[i]->stride_h < 0 || lt[i]->stride_t < 0)
             return fail(MPATTN_ERR_INVALID, "%s: null pointer or negative stride", ln[i]);
-    if (!p->workspace || (uintptr_t)p->workspace % 256)
-        return fail(MPATTN_ERR_INVALID, "workspace required (256-byte aligned)");
+    {
+        const int64_t need = mpattn::combine_bwd_workspace_bytes(p->B, p->H, p->L);
+        if (!p->workspace || (uintptr_t)p->workspace % 256 || p->workspace_bytes < need)
+            return fail(MPATTN_ERR_INVALID, "workspace: need %lld bytes, 256-byte aligned (got %lld)",
+                        (long long)need, (long long)p->workspace_bytes);
+    }
     hipError_t e = mpattn::launch_combine_bwd(*p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(MPATTN_ERR_LAUNCH, "combine bwd launch: %s", hipGetErrorString(e));
     return MPATTN_OK;

@@ -35,9 +35,11 @@
 //    keys: both logits, selected per element), skip (all keys padded). Stages
 //    whose two subtiles share one pure pathway take the fast path.
 //  * Softmax in base 2 without a running max: p = exp2(s2) relative to a
-//    reference m_ref = 0. A stage whose row sum leaves (0, 2^64] takes a rare
-//    fix-up path that recomputes it against the stage's max and moves m_ref
-//    (the wavefront then subtracts m_ref with one FMA per logit).
+//    reference m_ref = 0. A stage whose row sum exceeds 2^64, or leaves the
+//    row's running sum at 0 (fp16: at most 2^-6, below which its
+//    probabilities are subnormal), takes a rare fix-up path that recomputes
+//    it against the stage's max and moves m_ref (the wavefront then
+//    subtracts m_ref with one FMA per logit).
 //  * Row sums come from v_dot2_f32_bf16 on the rounded probabilities (the
 //    values the PV MFMA consumes).
 #include <type_traits>
@@ -258,6 +260,11 @@ template <int D> struct FwdCfg {
 // path, which moves the row's reference max. 2^64 keeps every partial sum and
 // accumulator far from fp32 overflow.
 constexpr float kSumHi = 18446744073709551616.0f;
+// fp16 probabilities lose precision below 2^-14 (subnormal) and overflow past
+// 65504: a row whose accumulated sum is still at most 2^-6 also takes the
+// fix-up, which then lowers the reference toward the row's logits. (bf16
+// shares fp32's exponent range: only an empty sum is sent there.)
+template <typename T> constexpr float sum_lo() { return std::is_same<T, fp16_t>::value ? 0.015625f : 0.0f; }
 
 template <int N> using IC = std::integral_constant<int, N>;
 
@@ -290,6 +297,7 @@ void fwd_kernel(const FwdArgs args) {
     constexpr int NJ = (TOT + W - 1) / W;    // per wavefront (the last may be idle)
     // With fused RoPE the logit factor scale*log2(e) is folded into Q.
     constexpr bool FOLDED = ROPE;
+    constexpr float kSumLo = sum_lo<T>();
     const mpattn_fwd_params& p = args.p;
 
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * S::STAGE];
@@ -663,8 +671,17 @@ void fwd_kernel(const FwdArgs args) {
         const float lq = l_run[u] + __shfl_xor(l_run[u], 32);
         const float ms = mq * c;
         float m_new;
-        if (lq > 0.f) m_new = fmaxf(m_ref[u], ms);
-        else m_new = ms > -INFINITY ? ms : m_ref[u];
+        if (lq > kSumLo) {
+            m_new = fmaxf(m_ref[u], ms);  // raise only
+        } else if (lq > 0.f) {
+            // Small accumulated sum (fp16): every earlier base-2 logit is at
+            // most m_ref + log2(lq) (halved for sqrt-softmax, whose sum holds
+            // squares), so lowering the reference to that bound keeps the
+            // rescaled sum at most 1.
+            m_new = fmaxf(ms, m_ref[u] + (SQRT ? 0.5f : 1.0f) * __log2f(lq));
+        } else {
+            m_new = ms > -INFINITY ? ms : m_ref[u];
+        }
         const float alpha = lq > 0.f ? fast_exp2(m_ref[u] - m_new) : 1.0f;
         l_run[u] *= SQRT ? alpha * alpha : alpha;
 #pragma unroll
@@ -677,7 +694,7 @@ void fwd_kernel(const FwdArgs args) {
     };
     // Check: true if any lane of block u needs the fix-up.
     auto needs_fix = [&](float ls, float lr) {
-        const bool bad = !(ls <= kSumHi) || (lr + ls == 0.f);
+        const bool bad = !(ls <= kSumHi) || (lr + ls <= kSumLo);
         return __builtin_amdgcn_ballot_w64(bad) != 0;
     };
 

@@ -49,16 +49,19 @@ class RotaryEmbedding(torch.nn.Module):
     def tables(self, seq_len, device, dtype=torch.float32):
         """(1, T, D) cos and sin of emb = cat(t * inv_freq, t * inv_freq); the
         angle is an fp32 product, cos/sin are evaluated in ``dtype`` (fp32 or
-        fp64)."""
-        key = (int(seq_len), device, dtype)
+        fp64). One table per (device, dtype) is kept, at the largest length
+        seen (rounded up to 256 positions); shorter lengths read its first T
+        positions, so variable-length inputs do not grow the cache."""
+        key = (device, dtype)
         hit = self._cache.get(key)
-        if hit is None:
-            t = torch.arange(seq_len, device=device, dtype=torch.float32)
+        if hit is None or hit[0].shape[1] < seq_len:
+            n = (int(seq_len) + 255) // 256 * 256
+            t = torch.arange(n, device=device, dtype=torch.float32)
             freqs = (t[:, None] * _inv_freq(self.dim, device)[None, :]).to(dtype)
             emb = torch.cat((freqs, freqs), dim=-1)
             hit = (emb.cos()[None], emb.sin()[None])
             self._cache[key] = hit
-        return hit
+        return hit[0][:, :seq_len], hit[1][:, :seq_len]
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """Rotate x (..., T, D); computed in fp32 (fp64 for fp64 inputs) and

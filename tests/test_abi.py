@@ -37,7 +37,7 @@ def test_exports_every_header_function(lib):
 
 
 def test_version_and_strings(lib):
-    assert lib.mpattn_version() == 3
+    assert lib.mpattn_version() == 4
     assert lib.mpattn_strerror(0) == b"success"
     assert lib.mpattn_strerror(-2) == b"unsupported configuration"
     assert lib.mpattn_strerror(-99) == b"unknown error"
@@ -175,6 +175,53 @@ def test_bwd_validation(lib):
     p.lse = 1 << 25
     p.D = 40
     assert lib.mpattn_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_UNSUPPORTED
+    p.D = 32
+    # workspace missing, undersized, misaligned
+    assert lib.mpattn_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
+    assert "workspace" in lib.mpattn_last_error().decode()
+    need = lib.mpattn_bwd_workspace_size(2, 20, 64, 32)
+    p.workspace_bytes = need - 1
+    assert lib.mpattn_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
+    assert "workspace" in lib.mpattn_last_error().decode()
+    p.workspace, p.workspace_bytes = (1 << 24) + 8, need
+    assert lib.mpattn_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
+    p.workspace = 1 << 24
+
+
+def _bwd_params(**over):
+    p = _lib.BwdParams()
+    for n in ("q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi", "out", "grad_out",
+              "dq_self", "dk_self", "dv_self", "dq_multi", "dk_multi", "dv_multi"):
+        setattr(p, n, _fake())
+    p.chain_id = 1 << 21
+    p.lse = 1 << 25
+    p.B, p.H, p.L, p.D = 2, 20, 64, 32
+    p.dtype, p.rope, p.scale = _lib.MPATTN_BF16, _lib.MPATTN_ROPE_NONE, 1.0
+    p.workspace, p.workspace_bytes = 1 << 24, 1 << 40
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("name", ["q_self", "grad_out", "out", "dk_multi", "dv_self"])
+def test_bwd_rejects_rows_past_32bit_offsets(lib, name):
+    """Every one of the 14 backward tensors: a row stride that puts row L-1
+    past 2^31 bytes from the (b, h) base is refused (the DMA offsets are
+    32-bit), before anything is enqueued."""
+    L = 64
+    stride_t = (1 << 31) // (L * 2) + 8
+    p = _bwd_params(**{name: _lib.Tensor4(1 << 20, 0, 0, stride_t)})
+    assert lib.mpattn_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_UNSUPPORTED
+    assert "32-bit row offsets" in lib.mpattn_last_error().decode()
+    assert name in lib.mpattn_last_error().decode()
+
+
+def test_bwd_rejects_dense_mask_past_32bit_offsets(lib):
+    L = 64
+    p = _bwd_params(chain_id=None, chain_mask=1 << 23, mask_stride_b=0,
+                    mask_stride_q=(1 << 31) // L + 16, mask_stride_k=1)
+    assert lib.mpattn_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_UNSUPPORTED
+    assert "chain_mask" in lib.mpattn_last_error().decode()
 
 
 def test_python_api_rejects_cpu_tensors():
@@ -248,8 +295,13 @@ def test_combine_bwd_validation(lib):
     assert lib.mpattn_combine_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
     assert "workspace" in lib.mpattn_last_error().decode()
     p.workspace = (1 << 24) + 128
+    p.workspace_bytes = 1 << 30
     assert lib.mpattn_combine_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
     p.workspace = 1 << 24
+    p.workspace_bytes = lib.mpattn_combine_bwd_workspace_size(2, 20, 64, 32) - 1
+    assert lib.mpattn_combine_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
+    assert "need" in lib.mpattn_last_error().decode()
+    p.workspace_bytes = 1 << 30
     p.dropout_p = 1.5
     assert lib.mpattn_combine_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_INVALID
     assert "dropout" in lib.mpattn_last_error().decode()
@@ -267,7 +319,8 @@ def test_combine_struct_layout():
     assert f.B.offset == f.mask_stride_k.offset + 8
     b = _lib.CombineBwdParams
     assert b.d_inter_values.offset == 8 * 32 and b.chain_mask.offset == 9 * 32
-    assert b.B.offset == b.workspace.offset + 8
+    assert b.workspace_bytes.offset == b.workspace.offset + 8
+    assert b.B.offset == b.workspace_bytes.offset + 8
 
 
 def test_combine_python_rejects_non_bool_mask():
@@ -296,3 +349,4 @@ def test_resolve_dropout():
     b = _resolve_dropout(0.1, True)
     c = _resolve_dropout(0.1, True)
     assert a == b and a != c
+

@@ -163,26 +163,59 @@ def test_hip_paths_have_no_cpu_fallback():
                 layer(x, chain_ids=cid)
 
 
-def test_project_qkv_weight_cache():
-    """project_qkv with separate q/k/v projections: in inference the
-    concatenated weight is reused across calls and rebuilt after an in-place
-    update; with gradients the concatenation stays in the graph."""
+def test_project_qkv_separate_projections():
+    """project_qkv with separate q/k/v projections returns their three
+    (T, B, E) outputs (the fused kernels read them by strides): nothing is
+    cached, so a weight write through ``.data`` takes effect at once, and a
+    call under inference_mode leaves nothing behind that a later call with
+    gradients would trip over."""
     from mint_plus_amd.attention import MultiHeadAttention
     torch.manual_seed(5)
     mha = MultiHeadAttention(16, 2)
     x = torch.randn(5, 3, 16)
-    ref = torch.cat([mha.q_proj(x), mha.k_proj(x), mha.v_proj(x)], -1)
+    q, k, v = mha.project_qkv(x)
+    torch.testing.assert_close(q, mha.q_proj(x))
+    torch.testing.assert_close(v, mha.v_proj(x))
     with torch.no_grad():
-        a = mha.project_qkv(x)
-        w_first = mha._qkv_cache[1]
-        b = mha.project_qkv(x)
-        assert mha._qkv_cache[1] is w_first
-        torch.testing.assert_close(a, ref.detach())
-        torch.testing.assert_close(b, ref.detach())
-        mha.k_proj.weight.add_(0.5)
-        c = mha.project_qkv(x)
-        assert mha._qkv_cache[1] is not w_first
-        torch.testing.assert_close(c[..., 16:32], mha.k_proj(x))
+        mha.k_proj.weight.data.mul_(0)
+        mha.k_proj.bias.data.fill_(2.0)
+    _, k2, _ = mha.project_qkv(x)
+    assert torch.all(k2 == 2.0)
+    with torch.inference_mode():
+        mha.project_qkv(x)
+    for prm in mha.parameters():
+        prm.requires_grad_(False)
+    xg = x.clone().requires_grad_(True)
+    sum(t.sum() for t in mha.project_qkv(xg)).backward()
+    assert xg.grad is not None
+    for prm in mha.parameters():
+        prm.requires_grad_(True)
     out = mha.project_qkv(x)
-    out.sum().backward()
+    sum(t.sum() for t in out).backward()
     assert mha.q_proj.weight.grad is not None and mha.v_proj.bias.grad is not None
+
+
+def test_rope_tables_do_not_grow_with_lengths():
+    """One cos/sin table per (D, device) for the kernels, and per
+    (device, dtype) in RotaryEmbedding, at the largest length seen: many
+    distinct lengths leave one entry, and a shorter length reads the prefix
+    of the longer table (the values depend on the position only)."""
+    from mint_plus_amd import _lib
+    from mint_plus_amd.rotary_embedding import RotaryEmbedding
+    _lib._rope_cache.clear()
+    for L in (17, 300, 64, 999, 5):
+        cos, sin = _lib.rope_tables(L, 32, "cpu")
+        assert cos.shape == (L, 16) and cos.is_contiguous()
+    assert len(_lib._rope_cache) == 1
+    full, _ = _lib.rope_tables(999, 32, "cpu")
+    short, _ = _lib.rope_tables(5, 32, "cpu")
+    assert torch.equal(short, full[:5])
+    rot = RotaryEmbedding(32)
+    for T in (9, 400, 33, 700):
+        c, s = rot.tables(T, torch.device("cpu"))
+        assert c.shape == (1, T, 32)
+    assert len(rot._cache) == 1
+    c1, _ = rot.tables(33, torch.device("cpu"))
+    t = torch.arange(33, dtype=torch.float32)
+    ang = t[:, None] * rot.inv_freq[None, :]
+    torch.testing.assert_close(c1[0, :, :16], ang.cos())

@@ -1,0 +1,259 @@
+"""The GPU parity comparisons can fail (CPU only).
+
+For the forward and backward GPU parity cases of ``tests/test_fwd_gpu.py``
+and ``tests/test_bwd_gpu.py``, this runs the case's own input generator and
+the same comparison (``tests/parity.py``) on CPU oracle results and checks:
+
+* planted mistakes are rejected: zeroed or halved output, swapped V
+  pathways, one 256-query block zeroed, dropped RoPE (cases whose logits
+  RoPE moves by O(1)); for the backward, each of dQ/dK of either pathway
+  zeroed, dQ and dK swapped, dQ and dK halved, swapped pathways, one
+  256-query block of dQ_self zeroed, dropped RoPE;
+* the comparison accepts the oracle evaluated on the operands rounded as
+  the kernels round them (fused RoPE: rotated Q and K rounded to the input
+  dtype), so a correct kernel is not rejected by the rounding of its
+  operands.
+
+The oracle here is ``oracle/torch_ref.py`` in float64 (pinned to the numpy
+oracle in ``tests/test_oracle.py``), with torch autograd for gradients. For
+the full-size shapes the check runs on a slice of the same inputs (sample 0,
+and heads 0-3 at the 3B shape): samples and heads are independent and
+identically distributed, and a mistake that every element shares is
+rejected on any slice.
+"""
+import numpy as np
+import pytest
+import torch
+
+import parity as P
+import test_bwd_gpu as BW
+import test_fwd_gpu as FW
+from oracle import mpattn_oracle as orc
+from oracle import torch_ref
+
+
+def _block(B, H, L):
+    """(b, h, query slice) of the 256-query block a planted mistake zeroes."""
+    q0 = 256 if L >= 512 else 0
+    return B - 1, H - 1, slice(q0, min(L, q0 + 256))
+
+
+def check_fwd_case(xs, cid, kp, rope, scale, dtype=torch.bfloat16, rope_matters=False,
+                   rounded_ref=False):
+    """rounded_ref: the GPU test compares against the oracle on the rounded
+    operands (``parity.round_operands``), so that is the reference here."""
+    B, H, L, D = xs[0].shape
+    exact = P.ref_forward(xs, cid, kp, rope, scale)
+    # a correct kernel's operand rounding passes
+    em, sc = P.round_operands(xs, D, scale, rope, dtype)
+    emo = P.ref_forward([torch.from_numpy(e) for e in em], cid, kp, False, sc)
+    if rounded_ref:
+        ref = emo
+        rel = np.linalg.norm(emo - exact) / np.linalg.norm(exact)
+        assert rel < 2e-2, rel   # the rounding is a small perturbation of the exact result
+    else:
+        ref = exact
+        assert P.compare16(emo, ref) is None, P.compare16(emo, ref)
+    bad = {"zero": ref * 0, "half": ref * 0.5}
+    blk = ref.copy()
+    b, h, qs = _block(B, H, L)
+    blk[b, h, qs] = 0
+    bad["block"] = blk
+    bad["swap_v"] = P.ref_forward(xs, cid, kp, rope, scale, swap_v=True)
+    if rope_matters:
+        bad["no_rope"] = P.ref_forward(xs, cid, kp, False, scale)
+    passed = [k for k, v in bad.items() if P.compare16(v, ref) is None]
+    assert not passed, f"planted mistakes not rejected: {passed}"
+
+
+def _worst_ratio(got, ref):
+    """Largest |got - ref| / (atol + rtol |ref|) over the gradient tensors."""
+    return max(float((np.abs(g - r) / (P.ATOL16 + P.RTOL16 * np.abs(r))).max()) for g, r in zip(got, ref))
+
+
+def check_bwd_case(xs, go, cid, kp, rope, scale, dtype=torch.bfloat16, rope_matters=False,
+                   rounded_ref=False, sqrt=False, mistakes=True):
+    """rounded_ref: the GPU test's reference is autograd with the rotated
+    Q_self/K_self rounded to dtype (``parity.ref_grads``). The backward's
+    rounding model (``parity.emulate_bwd16``) must stay within half the
+    bound of the reference (the calibration of each case's dO scale)."""
+    B, H, L, D = xs[0].shape
+    if sqrt:
+        a = [x.double().numpy() for x in xs]
+        ref = orc.mpattn_backward(*a, go.double().numpy(), chain_ids=cid, key_pad=kp, rope=rope,
+                                  scale=scale, sqrt_softmax=True)
+    else:
+        ref = P.ref_grads(xs, go, cid, kp, rope, scale, round_dtype=dtype if rounded_ref else None)
+    em = P.emulate_bwd16(xs, go, cid, kp, rope, scale, dtype, sqrt_softmax=sqrt)
+    ratio = _worst_ratio(em, ref)
+    assert ratio <= 0.5, f"rounding model uses {ratio:.2f} of the bound"
+    if rounded_ref:
+        exact = P.ref_grads(xs, go, cid, kp, rope, scale)
+        for r, x in zip(ref, exact):
+            rel = np.linalg.norm(r - x) / np.linalg.norm(x)
+            assert rel < 2e-2, rel   # operand rounding: a small perturbation
+    if not mistakes:
+        return
+    names = P.GRAD_NAMES
+    cands = {}
+    for i in (0, 1, 3, 4):
+        g = list(ref)
+        g[i] = g[i] * 0
+        cands[f"zero_{names[i]}"] = g
+    g = list(ref)
+    g[0], g[1], g[3], g[4] = ref[1], ref[0], ref[4], ref[3]
+    cands["swap_dq_dk"] = g
+    g = list(ref)
+    for i in (0, 1, 3, 4):
+        g[i] = g[i] * 0.5
+    cands["half_dq_dk"] = g
+    g = list(ref)
+    blk = ref[0].copy()
+    b, h, qs = _block(B, H, L)
+    blk[b, h, qs] = 0
+    g[0] = blk
+    cands["block_dq_self"] = g
+    cands["swap_pathways"] = P.ref_grads(xs, go, cid, kp, rope, scale, swap_v=True)
+    if rope_matters:
+        cands["no_rope"] = P.ref_grads(xs, go, cid, kp, False, scale)
+    passed = [k for k, v in cands.items() if not P.compare_grads16(v, ref)]
+    assert not passed, f"planted mistakes not rejected: {passed}"
+
+
+# ---------------------------------------------------------------- forward
+
+@pytest.mark.parametrize("D,L", FW.SMALL)
+def test_power_fwd_small(D, L):
+    xs, cid, kp = FW.small_case(D, L)
+    check_fwd_case(xs, cid, kp, True, D ** -0.5)
+
+
+@pytest.mark.parametrize("n", FW.CHAIN_COUNTS)
+def test_power_fwd_chains(n):
+    xs, cid, kp = FW.chain_case(n)
+    check_fwd_case(xs, cid, kp, True, 32 ** -0.5)
+
+
+@pytest.mark.parametrize("B,H,L,D,nchains,dense", FW.DISPATCH)
+def test_power_fwd_dispatch(B, H, L, D, nchains, dense):
+    xs, cid, kp = FW.dispatch_case(B, H, L, D, nchains)
+    check_fwd_case(xs, cid, kp, True, D ** -0.5)
+
+
+@pytest.mark.parametrize("D", FW.ROPE_SHARP)
+def test_power_fwd_rope_sharp(D):
+    xs, cid, kp = FW.rope_sharp_case(D)
+    check_fwd_case(xs, cid, kp, True, D ** -0.5, rope_matters=True, rounded_ref=True)
+
+
+def test_power_fwd_headline():
+    xs, cid, kp = FW.headline_case()
+    D = xs[0].shape[3]
+    check_fwd_case([x[:1] for x in xs], cid[:1], kp[:1], True, D ** -0.5)
+
+
+@pytest.mark.parametrize("B,H,L,D", FW.CFG3B)
+def test_power_fwd_3b(B, H, L, D):
+    xs, cid, kp = FW.case3b(B, H, L, D)
+    check_fwd_case([x[:1, :4] for x in xs], cid[:1], kp[:1], True, D ** -0.5)
+
+
+# ---------------------------------------------------------------- backward
+
+@pytest.mark.parametrize("D,L", BW.SMALL)
+def test_power_bwd_small(D, L):
+    xs, go, cid, kp = BW.small_case(D, L)
+    check_bwd_case(xs, go, cid, kp, True, D ** -0.5)
+
+
+@pytest.mark.parametrize("n", [3, 5])
+def test_power_bwd_chains(n):
+    xs, go, cid, kp = BW.chain_case(n)
+    check_bwd_case(xs, go, cid, kp, True, 32 ** -0.5)
+
+
+@pytest.mark.parametrize("B,H,L,D,nchains,dense", BW.DISPATCH)
+def test_power_bwd_dispatch(B, H, L, D, nchains, dense):
+    xs, go, cid, kp = BW.dispatch_case(B, H, L, D, nchains)
+    check_bwd_case(xs, go, cid, kp, True, D ** -0.5)
+
+
+@pytest.mark.parametrize("D", BW.ROPE_SHARP)
+def test_power_bwd_rope_sharp(D):
+    xs, go, cid, kp = BW.rope_sharp_case(D)
+    check_bwd_case(xs, go, cid, kp, True, D ** -0.5, rope_matters=True, rounded_ref=True)
+
+
+def test_power_bwd_autograd():
+    xs, go, cid, kp = BW.autograd_case()
+    check_bwd_case(xs, go, cid, kp, True, 32 ** -0.5)
+
+
+def test_power_bwd_headline():
+    xs, go, cid, kp = BW.headline_case()
+    D = xs[0].shape[3]
+    b = BW.HEADLINE_SAMPLES[0]
+    sl = slice(b, b + 1)
+    check_bwd_case([x[sl] for x in xs], go[sl], cid[sl], kp[sl], True, D ** -0.5)
+
+
+@pytest.mark.parametrize("B,H,L,D", BW.CFG3B)
+def test_power_bwd_3b(B, H, L, D):
+    xs, go, cid, kp = BW.case3b(B, H, L, D)
+    check_bwd_case([x[:1, :4] for x in xs], go[:1, :4], cid[:1], kp[:1], True, D ** -0.5)
+
+
+@pytest.mark.parametrize("n", [1])
+def test_power_bwd_one_chain(n):
+    xs, go, cid, kp = BW.chain_case(n)
+    check_bwd_case(xs, go, cid, kp, True, 32 ** -0.5, mistakes=False)
+
+
+@pytest.mark.parametrize("D", [32, 64])
+def test_power_bwd_dense_norope(D):
+    xs, go, cid, kp = BW.dense_norope_case(D)
+    check_bwd_case(xs, go, cid, kp, False, 1.0)
+
+
+@pytest.mark.parametrize("D", [16, 32, 64])
+def test_power_bwd_sqrt(D):
+    xs, go, cid, kp = BW.sqrt_case(D)
+    check_bwd_case(xs, go, cid, kp, True, D ** -0.5, sqrt=True, mistakes=False)
+
+
+@pytest.mark.parametrize("dtype,shift,spread,go_std", BW.RANGE)
+def test_power_bwd_range_calibration(dtype, shift, spread, go_std):
+    xs, go, cid, kp = BW.range_case(dtype, shift, spread, go_std)
+    check_bwd_case(xs, go, cid, kp, False, 1.0, dtype=dtype, mistakes=False)
+
+
+@pytest.mark.parametrize("L,D", [(256, 32), (200, 32), (1000, 32), (136, 64)])
+def test_power_bwd_dense_tiles(L, D):
+    xs, go, cid, kp = P.bwd_inputs(2, 2, L, D, torch.bfloat16, seed=41 + L + D, nchains=3)
+    check_bwd_case(xs, go, cid, kp, True, D ** -0.5)
+
+
+def test_power_bwd_all_padded_sample():
+    xs, go, cid, kp = P.bwd_inputs(2, 2, 96, 32, torch.bfloat16, seed=19, pad=False)
+    kp[1, :] = True
+    check_bwd_case(xs, go, cid, kp, True, 32 ** -0.5, mistakes=False)
+
+
+def test_power_bwd_fp16():
+    xs, go, cid, kp = P.bwd_inputs(2, 3, 190, 32, torch.float16, seed=17)
+    check_bwd_case(xs, go, cid, kp, True, 32 ** -0.5, dtype=torch.float16)
+
+
+def test_power_detects_planted_oracle_rope_mistake():
+    """A mistake planted in the oracle itself (RoPE sign flipped: the
+    rotation by -theta) is rejected by the fused-RoPE comparison."""
+    xs, cid, kp = FW.rope_sharp_case(32)
+    ref = P.ref_forward(xs, cid, kp, True, 32 ** -0.5)
+    L, D = xs[0].shape[2], 32
+    cos, sin = torch_ref.rope_tables(L, D, "cpu")
+    a = [x.double() for x in xs]
+    a[0] = torch_ref.apply_rope(a[0], cos, -sin)
+    a[1] = torch_ref.apply_rope(a[1], cos, -sin)
+    bad = P.ref_forward(a, cid, kp, False, 32 ** -0.5)
+    assert P.compare16(bad, ref) is not None
+    assert np.isfinite(ref).all()
