@@ -47,9 +47,13 @@ static inline int rup(int x, int m) { return (x + m - 1) / m * m; }
 //   ksum  int32 [B][Lp/32][4] key blocks: min, max chain (valid keys), #padded
 //   qcid  int32 [B][Lp]      query chain id (queries past L: 0)
 //   qsum  int32 [B][Lp/32][4] query blocks: min, max chain (queries < L)
-//   qrot, krot T [B][H][Lp][D]  RoPE-rotated Q_self / K_self (fused RoPE)
+//   qrot, krot, qmf T [B][H][Lp][D]  fused RoPE only: the forward's MFMA
+//                operands, rounded as the forward rounds them: Q_self rotated
+//                and multiplied by the logit factor, K_self rotated, Q_multi
+//                multiplied by the logit factor (so the logits recomputed here
+//                are the ones the forward's LSE was taken over)
 struct BwdWs {
-    int64_t lse2, delta, keff, ksum, qcid, qsum, qrot, krot, total;
+    int64_t lse2, delta, keff, ksum, qcid, qsum, qrot, krot, qmf, total;
 };
 
 static inline BwdWs bwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
@@ -65,7 +69,8 @@ static inline BwdWs bwd_ws_layout(int B, int H, int L, int D, int esize, bool ro
     w.qrot = al(w.qsum + (int64_t)B * (Lp / 32) * 16);
     const int64_t rot = rope ? (int64_t)B * H * Lp * D * esize : 0;
     w.krot = al(w.qrot + rot);
-    w.total = al(w.krot + rot);
+    w.qmf = al(w.krot + rot);
+    w.total = al(w.qmf + rot);
     return w;
 }
 
@@ -85,9 +90,13 @@ struct BwdArgs {
     const int* qsum;
     const void* qrot;
     const void* krot;
+    const void* qmf;  // folded Q_multi (fused RoPE)
+    float kmul;       // dK factor: scale, or scale / (logit factor) when Q is folded
     int Lp;
-    float c;     // logit factor: scale * log2(e), halved for sqrt-softmax
+    float c;     // logit factor: scale * log2(e), halved for sqrt-softmax (1 when
+                 // fused RoPE folds it into Q, as the forward does)
     float lmul;  // LSE factor: log2(e), halved for sqrt-softmax
+    float qmul;  // logit factor folded into Q by the prep kernel (fused RoPE)
     DropCfg drop;
     int mvec;  // dense mask rows readable as aligned 8-byte words
     int mdma;  // dense mask tiles copyable to LDS in 16-byte chunks (dK/dV)
@@ -104,7 +113,7 @@ template <int D> constexpr int kRotItems = (D / 2) % 8 == 0 ? D / 16 : 1;
 template <typename T, int D, bool ROPE, bool DENSE>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* lse2, float* delta,
                                                        int* keff, int* ksum, int* qcid, int* qsum,
-                                                       T* qrot, T* krot, int nchain, int nrow) {
+                                                       T* qrot, T* krot, T* qmf, int nchain, int nrow) {
     typedef typename Elt<T>::v8 v8;
     const mpattn_bwd_params& p = a.p;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -187,23 +196,27 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* l
         return;
     }
     if constexpr (ROPE) {
-        // Rotate rows of Q_self (first half of items) and K_self (second
-        // half); kRotItems<D> threads per row, each with an 8-dim chunk and
-        // its RoPE partner chunk (D = 24: one thread per row).
+        // The forward's MFMA operands (mpattn_fwd.hip, fused RoPE): Q_self
+        // rotated and times the logit factor, K_self rotated, Q_multi times
+        // the logit factor, each rounded once from the same fp32 values
+        // (rope_rot). Items: Q_self, K_self, Q_multi in thirds;
+        // kRotItems<D> threads per row, each with an 8-dim chunk and its
+        // RoPE partner chunk (D = 24: one thread per row).
         constexpr int H2 = D / 2, NPC = kRotItems<D>;
         const int64_t rows = (int64_t)p.B * p.H * Lp;
         int64_t item = (int64_t)(bid - nchain - nrow) * 256 + tid;
-        if (item >= 2 * rows * NPC) return;
-        const bool isk = item >= rows * NPC;
-        if (isk) item -= rows * NPC;
+        if (item >= 3 * rows * NPC) return;
+        const int which = (int)(item / (rows * NPC));  // 0 Q_self, 1 K_self, 2 Q_multi
+        item -= (int64_t)which * rows * NPC;
         const int64_t row = item / NPC;
         const int pc = (int)(item % NPC);
         const int t = (int)(row % Lp);
         const int bh = (int)(row / Lp);
         const int b = bh / p.H, h = bh % p.H;
-        const mpattn_tensor& src_t = isk ? p.k_self : p.q_self;
+        const mpattn_tensor& src_t = which == 0 ? p.q_self : which == 1 ? p.k_self : p.q_multi;
         const T* src = (const T*)src_t.ptr + b * src_t.stride_b + h * src_t.stride_h + (int64_t)t * src_t.stride_t;
-        T* dst = (isk ? krot : qrot) + row * D;
+        T* dst = (which == 0 ? qrot : which == 1 ? krot : qmf) + row * D;
+        const float mul = which == 1 ? 1.0f : a.qmul;
         if constexpr (H2 % 8 == 0) {
             const int d0 = pc * 8;
             float lo[8], hi[8];
@@ -211,12 +224,20 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* l
                 float x[8], y[8];
                 load8f<T>(src, d0, x);
                 load8f<T>(src, d0 + H2, y);
-                const float* cr = p.rope_cos + (int64_t)t * H2 + d0;
-                const float* sr = p.rope_sin + (int64_t)t * H2 + d0;
+                if (which == 2) {
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    lo[u] = x[u] * cr[u] - y[u] * sr[u];
-                    hi[u] = y[u] * cr[u] + x[u] * sr[u];
+                    for (int u = 0; u < 8; ++u) {
+                        lo[u] = x[u] * mul;
+                        hi[u] = y[u] * mul;
+                    }
+                } else {
+                    const float* cr = p.rope_cos + (int64_t)t * H2 + d0;
+                    const float* sr = p.rope_sin + (int64_t)t * H2 + d0;
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        lo[u] = rope_rot(x[u], y[u], cr[u], sr[u], true) * mul;
+                        hi[u] = rope_rot(y[u], x[u], cr[u], sr[u], false) * mul;
+                    }
                 }
             } else {
 #pragma unroll
@@ -228,7 +249,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* l
 #pragma unroll
             for (int d0 = 0; d0 < D; d0 += 8) {
                 float x[8];
-                if (t < L) load8_rot<T, D>(src, p.rope_cos, p.rope_sin, t, d0, 1.0f, true, x);
+                if (t < L) load8_rot<T, D>(src, p.rope_cos, p.rope_sin, t, d0, mul, which != 2, x);
                 else
                     for (int u = 0; u < 8; ++u) x[u] = 0.f;
                 *reinterpret_cast<v8*>(dst + d0) = pack8<T>(x);
@@ -351,7 +372,8 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     auto base = [&](const mpattn_tensor& t) { return (const T*)t.ptr + b * t.stride_b + h * t.stride_h; };
     const T* const qs_p = ROPE ? (const T*)a.qrot + (int64_t)bh * Lp * D : base(p.q_self);
     const int64_t qs_t = ROPE ? D : p.q_self.stride_t;
-    const T* const qm_p = base(p.q_multi);
+    const T* const qm_p = ROPE ? (const T*)a.qmf + (int64_t)bh * Lp * D : base(p.q_multi);
+    const int64_t qm_t = ROPE ? D : p.q_multi.stride_t;
     const T* const do_p = base(p.grad_out);
     const T* const ks_p = ROPE ? (const T*)a.krot + (int64_t)bh * Lp * D : base(p.k_self);
     const int64_t ks_t = ROPE ? D : p.k_self.stride_t;
@@ -423,7 +445,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
         int r, cb;
         dma_slot(j, r, cb);
         const T* tb = ten == 0 ? qs_p : ten == 1 ? qm_p : do_p;
-        const int64_t ts = ten == 0 ? qs_t : ten == 1 ? p.q_multi.stride_t : p.grad_out.stride_t;
+        const int64_t ts = ten == 0 ? qs_t : ten == 1 ? qm_t : p.grad_out.stride_t;
         dsb[j] = (const char*)tb;
         dstr[j] = (unsigned)(ts * (int64_t)sizeof(T));
         dlds[j] = ten * TS::TILE + part * 1024;
@@ -691,12 +713,11 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     stage_barrier();  // stage buffers become epilogue scratch
 
     float* scratch = (float*)(smem + wave * 32 * 65 * 4);
-    const float scale = p.scale;
     const float vmul = DROP ? a.drop.rkeep : 1.0f;
     store_rows<T, D, false>(dv[0], scratch, p.dv_self, b, h, kw0, L, vmul, false, nullptr, nullptr);
     store_rows<T, D, false>(dv[1], scratch, p.dv_multi, b, h, kw0, L, vmul, false, nullptr, nullptr);
-    store_rows<T, D, false>(dk[0], scratch, p.dk_self, b, h, kw0, L, scale, ROPE, p.rope_cos, p.rope_sin);
-    store_rows<T, D, false>(dk[1], scratch, p.dk_multi, b, h, kw0, L, scale, false, nullptr, nullptr);
+    store_rows<T, D, false>(dk[0], scratch, p.dk_self, b, h, kw0, L, a.kmul, ROPE, p.rope_cos, p.rope_sin);
+    store_rows<T, D, false>(dk[1], scratch, p.dk_multi, b, h, kw0, L, a.kmul, false, nullptr, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -737,7 +758,8 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     auto base = [&](const mpattn_tensor& t) { return (const T*)t.ptr + b * t.stride_b + h * t.stride_h; };
     const T* const qs_p = ROPE ? (const T*)a.qrot + (int64_t)bh * Lp * D : base(p.q_self);
     const int64_t qs_t = ROPE ? D : p.q_self.stride_t;
-    const T* const qm_p = base(p.q_multi);
+    const T* const qm_p = ROPE ? (const T*)a.qmf + (int64_t)bh * Lp * D : base(p.q_multi);
+    const int64_t qm_t = ROPE ? D : p.q_multi.stride_t;
     const T* const do_p = base(p.grad_out);
     const T* const ks_p = ROPE ? (const T*)a.krot + (int64_t)bh * Lp * D : base(p.k_self);
     const int64_t ks_t = ROPE ? D : p.k_self.stride_t;
@@ -757,7 +779,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
         if (ok) load8f<T>(qs_p + (int64_t)q * qs_t, d0, x);
         else for (int u = 0; u < 8; ++u) x[u] = 0.f;
         qf[0][kk] = pack8<T>(x);
-        if (ok) load8f<T>(qm_p + (int64_t)q * p.q_multi.stride_t, d0, x);
+        if (ok) load8f<T>(qm_p + (int64_t)q * qm_t, d0, x);
         else for (int u = 0; u < 8; ++u) x[u] = 0.f;
         qf[1][kk] = pack8<T>(x);
         if (ok) load8f<T>(do_p + (int64_t)q * p.grad_out.stride_t, d0, x);
@@ -1061,7 +1083,13 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     a.p = p;
     const int Lp = rup(p.L, kBS);
     a.Lp = Lp;
-    a.c = p.scale * kLog2e * (SQRT ? 0.5f : 1.0f);
+    // With fused RoPE the forward folds the logit factor into Q (both
+    // pathways); the backward recomputes the logits from the same folded,
+    // rounded operands (prep kernel), so c = 1 and dK = (scale / f) dS^T Qf.
+    const float f = p.scale * kLog2e * (SQRT ? 0.5f : 1.0f);
+    a.c = ROPE ? 1.0f : f;
+    a.qmul = f;
+    a.kmul = ROPE ? p.scale / f : p.scale;
     a.lmul = kLog2e * (SQRT ? 0.5f : 1.0f);
     a.drop = drop_cfg(p.dropout_p, p.dropout_seed);
     a.mvec = p.chain_mask && p.mask_stride_k == 1 && (uintptr_t)p.chain_mask % 8 == 0 && p.mask_stride_b % 8 == 0 &&
@@ -1078,6 +1106,7 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     int* qsum = (int*)(w + ws.qsum);
     T* qrot = (T*)(w + ws.qrot);
     T* krot = (T*)(w + ws.krot);
+    T* qmf = (T*)(w + ws.qmf);
     a.lse2 = lse2;
     a.delta = delta;
     a.keff = keff;
@@ -1086,11 +1115,12 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     a.qsum = qsum;
     a.qrot = qrot;
     a.krot = krot;
+    a.qmf = qmf;
     const int nchain = (p.B * (Lp / 64) + 3) / 4;
     const int nrow = (int)(((int64_t)p.B * p.H * Lp * kPrepLanes<D> + 255) / 256);
-    const int nrot = ROPE ? (int)((2 * (int64_t)p.B * p.H * Lp * kRotItems<D> + 255) / 256) : 0;
+    const int nrot = ROPE ? (int)((3 * (int64_t)p.B * p.H * Lp * kRotItems<D> + 255) / 256) : 0;
     hipLaunchKernelGGL((bwd_prep_kernel<T, D, ROPE, DENSE>), dim3(nchain + nrow + nrot), dim3(256), 0, stream,
-                       a, lse2, delta, keff, ksum, qcid, qsum, qrot, krot, nchain, nrow);
+                       a, lse2, delta, keff, ksum, qcid, qsum, qrot, krot, qmf, nchain, nrow);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nb = (p.L + 32 * W - 1) / (32 * W);

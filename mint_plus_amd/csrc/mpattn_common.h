@@ -189,6 +189,14 @@ __device__ __forceinline__ void load8f(const T* row, int d0, float out[8]) {
     for (int t = 0; t < 8; ++t) out[t] = (float)x[t];
 }
 
+// One element of RoPE's half-split rotation: x*cos - partner*sin for a dim in
+// the lower half, x*cos + partner*sin for the upper half, as one fma. Every
+// kernel that rotates an operand goes through this, so the forward and the
+// backward round the same fp32 values to the same 16-bit operands.
+__device__ __forceinline__ float rope_rot(float x, float partner, float c, float s, bool lo) {
+    return __builtin_fmaf(x, c, (lo ? -partner : partner) * s);
+}
+
 // 8 elements [d0, d0+8) of RoPE(row) * mul at position `pos`, for head dim D
 // (half-split layout: dim d pairs with d +- D/2; emb = cat(freqs, freqs)).
 // Dims >= D read as 0.
@@ -222,12 +230,11 @@ __device__ __forceinline__ void load8_rot(const T* row, const float* cos_tab,
         const f32x4 c1 = *reinterpret_cast<const f32x4*>(cr + fi + 4);
         const f32x4 s0 = *reinterpret_cast<const f32x4*>(sr + fi);
         const f32x4 s1 = *reinterpret_cast<const f32x4*>(sr + fi + 4);
-        const float sg = lo ? -1.f : 1.f;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const float c = t < 4 ? c0[t & 3] : c1[t & 3];
             const float s = t < 4 ? s0[t & 3] : s1[t & 3];
-            out[t] = (x[t] * c + sg * y[t] * s) * mul;
+            out[t] = rope_rot(x[t], y[t], c, s, lo) * mul;
         }
     } else {
 #pragma unroll
@@ -237,8 +244,7 @@ __device__ __forceinline__ void load8_rot(const T* row, const float* cos_tab,
             const int dp = lo ? d + H2 : d - H2;
             const int fi = lo ? d : dp;
             const float y = (float)row[dp];
-            const float sg = lo ? -1.f : 1.f;
-            out[t] = (x[t] * cr[fi] + sg * y * sr[fi]) * mul;
+            out[t] = rope_rot(x[t], y, cr[fi], sr[fi], lo) * mul;
         }
     }
 }

@@ -35,13 +35,13 @@
 //    keys: both logits, selected per element), skip (all keys padded). Stages
 //    whose two subtiles share one pure pathway take the fast path.
 //  * Softmax in base 2 without a running max: p = exp2(s2) relative to a
-//    reference m_ref = 0. A stage whose row sum exceeds 2^64, or leaves the
-//    row's running sum at 0 (fp16: at most 2^-6, below which its
-//    probabilities are subnormal), takes a rare fix-up path that recomputes
+//    reference m_ref = 0. A stage whose row sum exceeds 2^64 (fp16: 2^15),
+//    or leaves the row's running sum at 0 (fp16: at most 2^-6, below which
+//    its probabilities are subnormal), takes a rare fix-up path that recomputes
 //    it against the stage's max and moves m_ref (the wavefront then
 //    subtracts m_ref with one FMA per logit).
-//  * Row sums come from v_dot2_f32_bf16 on the rounded probabilities (the
-//    values the PV MFMA consumes).
+//  * Row sums add the fp32 probabilities with VALU adds (v_dot2 would share
+//    the matrix-core issue path and serialise with the MFMAs).
 #include <type_traits>
 
 #include "mpattn_common.h"
@@ -204,8 +204,8 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p
                 const float* sr = p.rope_sin + (int64_t)t * H2 + d0;
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    lo[u] = x[u] * cr[u] - y[u] * sr[u];
-                    hi[u] = y[u] * cr[u] + x[u] * sr[u];
+                    lo[u] = rope_rot(x[u], y[u], cr[u], sr[u], true);
+                    hi[u] = rope_rot(y[u], x[u], cr[u], sr[u], false);
                 }
             } else {
 #pragma unroll
@@ -258,8 +258,12 @@ template <int D> struct FwdCfg {
 
 // Row sums above this bound (or not finite) send a stage through the fix-up
 // path, which moves the row's reference max. 2^64 keeps every partial sum and
-// accumulator far from fp32 overflow.
-constexpr float kSumHi = 18446744073709551616.0f;
+// accumulator far from fp32 overflow; for fp16, 2^15 keeps every probability
+// (each at most the sum) inside the fp16 range (max 65504) when it is
+// rounded for the PV MFMA.
+template <typename T> constexpr float sum_hi() {
+    return std::is_same<T, fp16_t>::value ? 32768.0f : 18446744073709551616.0f;
+}
 // fp16 probabilities lose precision below 2^-14 (subnormal) and overflow past
 // 65504: a row whose accumulated sum is still at most 2^-6 also takes the
 // fix-up, which then lowers the reference toward the row's logits. (bf16
@@ -298,6 +302,7 @@ void fwd_kernel(const FwdArgs args) {
     // With fused RoPE the logit factor scale*log2(e) is folded into Q.
     constexpr bool FOLDED = ROPE;
     constexpr float kSumLo = sum_lo<T>();
+    constexpr float kSumHi = sum_hi<T>();
     const mpattn_fwd_params& p = args.p;
 
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * S::STAGE];
@@ -474,11 +479,11 @@ void fwd_kernel(const FwdArgs args) {
 #pragma unroll
                         for (int t = 0; t < 8; ++t) x[t] = 0.f;
                     } else if (ROPE && pw == 0) {
-                        const float sg = d0 < H2 ? -1.f : 1.f;
+                        const bool lo = d0 < H2;
 #pragma unroll
                         for (int t = 0; t < 8; ++t) {
                             const float c = qcs[u][kk][t >> 2][t & 3], sn = qcs[u][kk][2 + (t >> 2)][t & 3];
-                            x[t] = ((float)qraw[u][pw][kk][t] * c + sg * (float)qpar[u][kk][t] * sn) * args.qmul;
+                            x[t] = rope_rot((float)qraw[u][pw][kk][t], (float)qpar[u][kk][t], c, sn, lo) * args.qmul;
                         }
                     } else {
 #pragma unroll
@@ -612,9 +617,12 @@ void fwd_kernel(const FwdArgs args) {
                      uint32_t dr) -> float {
         constexpr int NS = decltype(ns_c)::value;
         typedef float f32x2 __attribute__((ext_vector_type(2)));
-        // Pairs are rounded once (v_cvt_pk) and feed both the PV operand and
-        // the row sum; two sum chains halve the dependency depth.
-        float ls0 = 0.f, ls1 = 0.f;
+        // Pairs are rounded once (v_cvt_pk) for the PV operand. The row sum
+        // adds the fp32 probabilities with plain VALU adds: v_dot2 on the
+        // rounded pairs would issue on the matrix-core path and serialise
+        // with the MFMAs of the other wavefronts of the SIMD (measured), where
+        // adds run under them. Four sum chains keep the dependency depth low.
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int st = 0; st < NS; ++st)
 #pragma unroll
@@ -625,6 +633,13 @@ void fwd_kernel(const FwdArgs args) {
                     const f32x2 f = {prob(sv[st][8 * cc + 2 * uu], sh, mr),
                                      prob(sv[st][8 * cc + 2 * uu + 1], sh, mr)};
                     pr[uu] = __builtin_convertvector(f, v2);
+                    if constexpr (SQRT) {
+                        ls[uu] = fmaf(f.x, f.x, ls[uu]);
+                        ls[uu] = fmaf(f.y, f.y, ls[uu]);
+                    } else {
+                        ls[uu] += f.x;
+                        ls[uu] += f.y;
+                    }
                 }
                 v2 pv[4];
 #pragma unroll
@@ -642,19 +657,8 @@ void fwd_kernel(const FwdArgs args) {
                 pb[st][cc] = __builtin_shufflevector(__builtin_shufflevector(pv[0], pv[1], 0, 1, 2, 3),
                                                      __builtin_shufflevector(pv[2], pv[3], 0, 1, 2, 3), 0, 1, 2,
                                                      3, 4, 5, 6, 7);
-                if constexpr (SQRT) {
-                    ls0 = E::sq2(pr[0], ls0);
-                    ls1 = E::sq2(pr[1], ls1);
-                    ls0 = E::sq2(pr[2], ls0);
-                    ls1 = E::sq2(pr[3], ls1);
-                } else {
-                    ls0 = E::sum2(pr[0], ls0);
-                    ls1 = E::sum2(pr[1], ls1);
-                    ls0 = E::sum2(pr[2], ls0);
-                    ls1 = E::sum2(pr[3], ls1);
-                }
             }
-        return ls0 + ls1;
+        return (ls[0] + ls[1]) + (ls[2] + ls[3]);
     };
     // Rare path: a lane's stage sum overflowed, or its row has accumulated
     // nothing yet. The subtile's logits are recomputed from LDS (`logits`

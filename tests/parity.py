@@ -240,8 +240,11 @@ def round_st(x, dtype):
 
 def ref_grads(xs, go, cid, kp, rope, scale, swap_v=False, round_dtype=None):
     """Gradients of sum(out * go) w.r.t. the six inputs (torch autograd in
-    float64). With round_dtype and rope, the rotated Q_self/K_self are
-    rounded to round_dtype in the forward (the backward kernels' operands)."""
+    float64). With round_dtype and rope, the logits are taken over the
+    operands the 16-bit kernels feed their MFMAs with fused RoPE (both
+    passes): R(q_self) * f, q_multi * f (f = scale * log2 e, fp32) and
+    R(k_self), each rounded once to round_dtype; the rounding is the identity
+    for the gradient."""
     from oracle import torch_ref
     leaves = [x.double().requires_grad_(True) for x in xs]
     a = list(leaves)
@@ -250,8 +253,10 @@ def ref_grads(xs, go, cid, kp, rope, scale, swap_v=False, round_dtype=None):
     L, D = xs[0].shape[2], xs[0].shape[3]
     if round_dtype is not None and rope:
         cos, sin = torch_ref.rope_tables(L, D, "cpu")
-        a[0] = round_st(torch_ref.apply_rope(a[0], cos, sin), round_dtype)
+        f = float(np.float32(scale) * np.float32(1.4426950408889634))
+        a[0] = round_st(torch_ref.apply_rope(a[0], cos, sin) * f, round_dtype) / f
         a[1] = round_st(torch_ref.apply_rope(a[1], cos, sin), round_dtype)
+        a[3] = round_st(a[3] * f, round_dtype) / f
         rope = False
     out, _ = torch_ref.forward(*a, chain_ids=torch.from_numpy(cid), key_pad=torch.from_numpy(kp),
                                rope=rope, scale=scale, dtype=torch.float64, chunk=1)
@@ -269,7 +274,8 @@ def _rnd(x, dtype):
 def emulate_bwd16(xs, go, cid, kp, rope, scale, dtype, sqrt_softmax=False):
     """The six gradients computed the way the 16-bit backward kernels round
     (a model of their arithmetic, for calibrating the tests, not an oracle):
-    Q_self/K_self rotated in fp32 and rounded to ``dtype``; P from the exact
+    with fused RoPE the logits come from the forward's folded, rounded
+    operands (``ref_grads``); P from the exact
     LSE; dV = round(P)^T dO; dS = P (dP - Delta) (sqrt-softmax:
     W (dW - W Delta) / 2) rounded to ``dtype`` before dQ = scale dS K and
     dK = scale dS^T Q; Delta = rowsum(round(O) * dO); RoPE's transpose applied
@@ -279,15 +285,17 @@ def emulate_bwd16(xs, go, cid, kp, rope, scale, dtype, sqrt_softmax=False):
     a = [x.to(torch.float64) for x in xs]
     g = go.to(torch.float64)
     B, H, L, D = a[0].shape
-    qs, ks = a[0], a[1]
-    if rope:
+    qs, ks, qm = a[0], a[1], a[3]
+    if rope:  # the forward's folded, rounded operands (see ref_grads)
         cos, sin = torch_ref.rope_tables(L, D, "cpu")
-        qs = _rnd(torch_ref.apply_rope(qs, cos, sin).float().double(), dtype)
+        f = float(np.float32(scale) * np.float32(1.4426950408889634)) * (0.5 if sqrt_softmax else 1.0)
+        qs = _rnd(torch_ref.apply_rope(qs, cos, sin).float().double() * f, dtype) / f
         ks = _rnd(torch_ref.apply_rope(ks, cos, sin).float().double(), dtype)
+        qm = _rnd(qm * f, dtype) / f
     c = torch.from_numpy(cid)
     cross = (c[:, :, None] != c[:, None, :])[:, None]
     pad = torch.from_numpy(kp)[:, None, None, :]
-    s = torch.where(cross, scale * a[3] @ a[4].transpose(-1, -2), scale * qs @ ks.transpose(-1, -2))
+    s = torch.where(cross, scale * qm @ a[4].transpose(-1, -2), scale * qs @ ks.transpose(-1, -2))
     s = s.masked_fill(pad, float("-inf"))
     m = s.amax(-1, keepdim=True)
     m = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
@@ -306,7 +314,7 @@ def emulate_bwd16(xs, go, cid, kp, rope, scale, dtype, sqrt_softmax=False):
     dv_s = w16.masked_fill(cross, 0).transpose(-1, -2) @ g
     dv_m = w16.masked_fill(~cross, 0).transpose(-1, -2) @ g
     dq_s, dk_s = scale * ds_s @ ks, scale * ds_s.transpose(-1, -2) @ qs
-    dq_m, dk_m = scale * ds_m @ a[4], scale * ds_m.transpose(-1, -2) @ a[3]
+    dq_m, dk_m = scale * ds_m @ a[4], scale * ds_m.transpose(-1, -2) @ qm
     if rope:
         cos, sin = torch_ref.rope_tables(L, D, "cpu")
         h = D // 2
