@@ -28,8 +28,9 @@
  *
  * Conventions
  *   - The caller owns and allocates every device buffer (outputs and the
- *     backward workspace). The library never allocates, never synchronises,
- *     and keeps no mutable global state: calls on different streams are
+ *     workspaces). The library never allocates, never synchronises, and
+ *     keeps no mutable global state (apart from mpattn_fwd_noalloc's static
+ *     scratch and its per-device address): calls on different streams are
  *     independent.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
  *   - All tensors are 4-D (B, H, L, D) views given by a base pointer and
@@ -144,6 +145,19 @@ int64_t mpattn_fwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D, in
  * (mint_plus/models/kernels/multi_pathway_attention.py:184-279) and
  * fused_multi_pathway_attention_fp16 (multi_pathway_attention_fp16.py:148). */
 int mpattn_fwd(const mpattn_fwd_params *p, void *stream);
+
+/* No-allocation forward. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments and result
+ * as mpattn_fwd, except that workspace / workspace_bytes are ignored: the
+ * workspace is a static device array of MPATTN_NOALLOC_SCRATCH_BYTES bytes
+ * that the library holds on every GPU it runs on until the process ends.
+ * It calls no allocating routine. Shapes whose workspace
+ * (mpattn_fwd_workspace_size) exceeds the array return
+ * MPATTN_ERR_UNSUPPORTED. All calls on one GPU share the array: calls that
+ * overlap in time on one GPU (different streams or threads) race. */
+#define MPATTN_NOALLOC_SCRATCH_BYTES (48ll << 20)
+int mpattn_fwd_noalloc(const mpattn_fwd_params *p, void *stream);
 
 /* Workspace bytes mpattn_bwd needs for (B, H, L). */
 int64_t mpattn_bwd_workspace_size(int32_t B, int32_t H, int32_t L, int32_t D);

@@ -121,6 +121,7 @@ class CombineBwdParams(ctypes.Structure):
 # Functions declared in include/mpattn.h, with their ctypes signatures.
 EXPORTS = {
     "mpattn_fwd": (ctypes.c_int, [ctypes.POINTER(FwdParams), ctypes.c_void_p]),
+    "mpattn_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(FwdParams), ctypes.c_void_p]),
     "mpattn_bwd": (ctypes.c_int, [ctypes.POINTER(BwdParams), ctypes.c_void_p]),
     "mpattn_fwd_workspace_size": (ctypes.c_int64, [ctypes.c_int32] * 6),
     "mpattn_bwd_workspace_size": (ctypes.c_int64, [ctypes.c_int32] * 4),
@@ -286,13 +287,17 @@ def _aligned(t):
 def mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, *, chain_ids=None,
                chain_mask=None, key_padding_mask=None, rope=False, scale=1.0,
                sqrt_softmax=False, dropout_p=0.0, dropout_seed=0, out=None, need_lse=False,
-               lse=None):
+               lse=None, noalloc=False):
     """Launch the forward kernel on the current stream.
 
     Returns ``out`` (B, H, L, D) and, if ``need_lse``, the fp32 (B, H, L)
     log-sum-exp (natural units of the scaled logits). With ``dropout_p`` > 0
     the keep mask is a function of ``dropout_seed`` (a 64-bit integer) and the
     element's (b, h, query, key); the LSE is that of the undropped softmax.
+
+    ``noalloc`` calls ``mpattn_fwd_noalloc`` (the workspace is the library's
+    static device scratch, nothing is allocated; give ``out`` and, with
+    ``need_lse``, ``lse`` to allocate nothing here either).
     """
     ins = [q_self, k_self, v_self, q_multi, k_multi, v_multi]
     names = ["q_self", "k_self", "v_self", "q_multi", "k_multi", "v_multi"]
@@ -330,14 +335,19 @@ def mpattn_fwd(q_self, k_self, v_self, q_multi, k_multi, v_multi, *, chain_ids=N
     p.dropout_p = float(dropout_p)
     p.dropout_seed = int(dropout_seed) & 0xFFFFFFFFFFFFFFFF
     lib = load_library()
-    ws_bytes = lib.mpattn_fwd_workspace_size(B, H, L, D, p.dtype, p.rope)
-    if ws_bytes < 0:
-        raise MpattnError(MPATTN_ERR_INVALID, "mpattn_fwd_workspace_size", "bad shape")
-    # torch's caching allocator returns 512-byte aligned blocks
-    ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device=dev)
-    p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
-    rc = lib.mpattn_fwd(ctypes.byref(p), _stream_handle(dev))
-    _check(rc, "mpattn_fwd")
+    if noalloc:
+        ws = None
+        rc = lib.mpattn_fwd_noalloc(ctypes.byref(p), _stream_handle(dev))
+        _check(rc, "mpattn_fwd_noalloc")
+    else:
+        ws_bytes = lib.mpattn_fwd_workspace_size(B, H, L, D, p.dtype, p.rope)
+        if ws_bytes < 0:
+            raise MpattnError(MPATTN_ERR_INVALID, "mpattn_fwd_workspace_size", "bad shape")
+        # torch's caching allocator returns 512-byte aligned blocks
+        ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device=dev)
+        p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
+        rc = lib.mpattn_fwd(ctypes.byref(p), _stream_handle(dev))
+        _check(rc, "mpattn_fwd")
     del keep, ins, ws
     return (out, lse) if need_lse else out
 

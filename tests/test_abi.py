@@ -350,3 +350,18 @@ def test_resolve_dropout():
     c = _resolve_dropout(0.1, True)
     assert a == b and a != c
 
+
+def test_fwd_noalloc_rejects_shapes_beyond_scratch(lib):
+    """mpattn_fwd_noalloc validates like mpattn_fwd, then refuses a shape
+    whose workspace exceeds the static scratch, before touching the device."""
+    limit = 48 << 20
+    p = _fwd_params(B=8, H=40, L=2048, D=64)
+    need = lib.mpattn_fwd_workspace_size(8, 40, 2048, 64, _lib.MPATTN_BF16, _lib.MPATTN_ROPE_FUSED)
+    assert need > limit
+    assert lib.mpattn_fwd_noalloc(ctypes.byref(p), None) == _lib.MPATTN_ERR_UNSUPPORTED
+    msg = lib.mpattn_last_error().decode()
+    assert "static scratch" in msg and str(need) in msg and str(limit) in msg
+    p = _fwd_params(D=48)
+    assert lib.mpattn_fwd_noalloc(ctypes.byref(p), None) == _lib.MPATTN_ERR_UNSUPPORTED
+    assert "head dim" in lib.mpattn_last_error().decode()
+    assert lib.mpattn_fwd_noalloc(None, None) == _lib.MPATTN_ERR_INVALID
