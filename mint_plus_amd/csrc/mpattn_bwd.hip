@@ -40,6 +40,8 @@ constexpr int kBS = 64;  // rows per LDS stage
 
 static inline int rup(int x, int m) { return (x + m - 1) / m * m; }
 
+template <int N> using IC = std::integral_constant<int, N>;
+
 // Workspace layout (offsets 256-byte aligned), Lp = L rounded up to 64:
 //   lse2  f32   [B][H][Lp]   LSE * log2(e); +inf past L
 //   delta f32   [B][H][Lp]   dO . O; 0 past L
@@ -282,7 +284,7 @@ template <int D> struct BwdShape {
 template <typename T, int D, bool TRANS>
 __device__ void store_rows(const f32x16* acc, float* scratch, const mpattn_tensor& dst, int b, int h,
                            int r0, int L, float mul, bool rope, const float* cos_tab,
-                           const float* sin_tab) {
+                           const float* sin_tab, uint32_t rowmask = 0xffffffffu) {
     using BS = BwdShape<D>;
     typedef typename Elt<T>::v8 v8;
     const int lane = threadIdx.x & 63, hh = lane >> 5, ql = lane & 31;
@@ -306,9 +308,10 @@ __device__ void store_rows(const f32x16* acc, float* scratch, const mpattn_tenso
         const int r = r0 + row;
         if (r >= L) continue;
         float x[8];
+        const bool live = (rowmask >> row) & 1u;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = scratch[row * LD + d0 + u];
-        if (rope) {
+        for (int u = 0; u < 8; ++u) x[u] = live ? scratch[row * LD + d0 + u] : 0.f;
+        if (rope && live) {
             constexpr int H2 = D / 2;
             const float* cr = cos_tab + (int64_t)r * H2;
             const float* sr = sin_tab + (int64_t)r * H2;
@@ -348,7 +351,8 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     constexpr int MROW = 32 * W;
     constexpr int MSK = DENSE ? kBS * MROW : 0;
     constexpr int STAGE = NTEN * TS::TILE + AUX + MSK;
-    constexpr int NBUF = 2;
+    // Copies run NBUF-1 stages ahead (three buffers where they fit in 64 KB).
+    constexpr int NBUF = 3 * STAGE <= 65536 ? 3 : 2;
     static_assert(!DENSE || (kBS * MROW) % (1024 * W) == 0, "mask tile copies split evenly over the waves");
     const mpattn_bwd_params& p = a.p;
 
@@ -419,9 +423,14 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     const bool kvalid = ckey != kPadChain;
     const int kc_min = __builtin_amdgcn_readfirstlane(wave_min_i(kvalid ? ckey : INT32_MAX));
     const int kc_max = __builtin_amdgcn_readfirstlane(wave_max_i(kvalid ? ckey : INT32_MIN));
-    const bool any_pad = __builtin_amdgcn_ballot_w64(!kvalid) != 0;
+    // Padded keys are not masked in the loop: a lane's probabilities enter only
+    // its own key's rows of dV and dK, which the epilogue writes as zeros.
+    const uint32_t key_live = (uint32_t)__builtin_amdgcn_ballot_w64(kvalid);
+    const bool any_live = key_live != 0;
 
-    // ---- accumulators: [0] self, [1] multimer ----
+    // ---- accumulators: [0] self, [1] multimer. Each subtile pass updates
+    // both from one code block (the pathway it does not serve gets zero
+    // operands), so they keep one register home: no copies between passes.
     f32x16 dv[2][BS::NDB], dk[2][BS::NDB];
 #pragma unroll
     for (int pw = 0; pw < 2; ++pw)
@@ -429,7 +438,6 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
         for (int db = 0; db < BS::NDB; ++db)
 #pragma unroll
             for (int i = 0; i < 16; ++i) dv[pw][db][i] = dk[pw][db][i] = 0.f;
-
     // ---- DMA plan (as the forward) ----
     const char* dsb[NJ];
     unsigned dstr[NJ], dlds[NJ], dloff[NJ];
@@ -558,52 +566,16 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
         return acc;
     };
 
-    // One subtile of 32 queries; mode 0/1: pure pathway, 2: both pathways.
-    auto subtile = [&](const char* stage, int st, int mode, int q0) {
+    // One pass over a subtile of 32 queries on pathway pw. masked: only the
+    // pairs on pw count (a subtile with queries or keys on several chains
+    // takes one masked pass per pathway); the others get an infinite LSE,
+    // so their probabilities are 0.
+    auto pass = [&](bool masked, auto pw_c, const char* stage, int st, int q0) {
+        constexpr int pw = decltype(pw_c)::value;
         float l2[16], dl[16];
         aux16(stage, 0, st, l2);
         aux16(stage, 1, st, dl);
-        v8 qa[2][BS::NKK], doa[BS::NKK];
-#pragma unroll
-        for (int kk = 0; kk < BS::NKK; ++kk) doa[kk] = rop(stage, 2, st, kk);
-        f32x16 pm, dsm;  // P and dS in the selected pathway, per slot
-        bool same[16];
-        // Dropout: dP of dropped entries is 0, kept ones scaled by 1/(1-p);
-        // the dV operand is Z*P (the 1/(1-p) goes into the dV store).
-        bool keep[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) keep[i] = true;
-        if constexpr (DROP) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int qg = q0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8);
-                keep[i] = drop_keep(drop_row(a.drop.lo, (uint32_t)bh, (uint32_t)qg), a.drop.hi, (uint32_t)key,
-                                    a.drop.thr);
-            }
-        }
-        auto dpe = [&](float dp, int i) { return DROP ? (keep[i] ? dp * a.drop.rkeep : 0.f) : dp; };
-        if (mode != 2) {
-            const int pw = mode;
-#pragma unroll
-            for (int kk = 0; kk < BS::NKK; ++kk) qa[0][kk] = rop(stage, pw, st, kk);
-            const f32x16 sv = mma_kloop(qa[0], pw == 0 ? kf[0] : kf[1]);
-            const f32x16 dp = mma_kloop(doa, pw == 0 ? vf[0] : vf[1]);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                pm[i] = fast_exp2(fmaf(sv[i], c, -l2[i]));
-                dsm[i] = dscore(pm[i], dpe(dp[i], i), dl[i]);
-                same[i] = pw == 0;
-            }
-        } else {
-#pragma unroll
-            for (int kk = 0; kk < BS::NKK; ++kk) {
-                qa[0][kk] = rop(stage, 0, st, kk);
-                qa[1][kk] = rop(stage, 1, st, kk);
-            }
-            const f32x16 ss = mma_kloop(qa[0], kf[0]);
-            const f32x16 sm = mma_kloop(qa[1], kf[1]);
-            const f32x16 dps = mma_kloop(doa, vf[0]);
-            const f32x16 dpm = mma_kloop(doa, vf[1]);
+        if (masked) {
             int qc[16];
             {
                 float tmp[16];
@@ -613,7 +585,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
             }
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                bool sm_;
+                bool same;
                 if constexpr (DENSE) {
                     const int ql_ = st * 32 + 16 * (i / 8) + 8 * hh + (i % 8);
                     const int qg = q0 + ql_;
@@ -624,48 +596,58 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
                         mb = p.chain_mask[(int64_t)b * p.mask_stride_b + (int64_t)qg * p.mask_stride_q +
                                           (int64_t)key * p.mask_stride_k] != 0;
                     }
-                    sm_ = !(qg < L && kin && mb);
+                    same = !(qg < L && kin && mb);
                 } else {
-                    sm_ = qc[i] == ckey;
+                    same = qc[i] == ckey;
                 }
-                same[i] = sm_;
-                const float s = sm_ ? ss[i] : sm[i];
-                const float dp = sm_ ? dps[i] : dpm[i];
-                pm[i] = kvalid ? fast_exp2(fmaf(s, c, -l2[i])) : 0.f;
-                dsm[i] = dscore(pm[i], dpe(dp, i), dl[i]);
+                if (same != (pw == 0)) l2[i] = INFINITY;
             }
         }
-        // dV_pw += P^T dO ; dK_pw += dS^T Q_pw, per 16-query chunk cc
+        v8 qa[BS::NKK], doa[BS::NKK], ka[BS::NKK], va[BS::NKK];
+#pragma unroll
+        for (int kk = 0; kk < BS::NKK; ++kk) {
+            doa[kk] = rop(stage, 2, st, kk);
+            qa[kk] = rop(stage, pw, st, kk);
+            ka[kk] = pw ? kf[1][kk] : kf[0][kk];
+            va[kk] = pw ? vf[1][kk] : vf[0][kk];
+        }
+        const f32x16 sv = mma_kloop(qa, ka);
+        const f32x16 dp = mma_kloop(doa, va);
+        // Dropout: dP of dropped entries is 0, kept ones scaled by 1/(1-p);
+        // the dV operand is Z*P (the 1/(1-p) goes into the dV store).
+        float pv[16], dsv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float pm = fast_exp2(fmaf(sv[i], c, -l2[i]));
+            float dpi = dp[i];
+            bool keep = true;
+            if constexpr (DROP) {
+                const int qg = q0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8);
+                keep = drop_keep(drop_row(a.drop.lo, (uint32_t)bh, (uint32_t)qg), a.drop.hi, (uint32_t)key,
+                                 a.drop.thr);
+                dpi = keep ? dpi * a.drop.rkeep : 0.f;
+            }
+            dsv[i] = dscore(pm, dpi, dl[i]);
+            pv[i] = keep ? pm : 0.f;
+        }
+        // dV += P^T dO ; dK += dS^T Q for pathway pw, per 16-query chunk cc
+        // (the other pathway's MFMAs take zero operands)
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-            v8 ps, pmv, dss, dsmv;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const int i = 8 * cc + t;
-                const T pv = (T)(keep[i] ? pm[i] : 0.f), dv_ = (T)dsm[i];
-                ps[t] = same[i] ? pv : (T)0.f;
-                pmv[t] = same[i] ? (T)0.f : pv;
-                dss[t] = same[i] ? dv_ : (T)0.f;
-                dsmv[t] = same[i] ? (T)0.f : dv_;
-            }
+            const v8 p8 = pack8<T>(pv + 8 * cc), ds8 = pack8<T>(dsv + 8 * cc);
 #pragma unroll
             for (int db = 0; db < BS::NDB; ++db) {
-                const v8 dot = top(stage, 2, st, cc, db);
-                if (mode != 1) {
-                    dv[0][db] = E::mma(ps, dot, dv[0][db]);
-                    dk[0][db] = E::mma(dss, top(stage, 0, st, cc, db), dk[0][db]);
-                }
-                if (mode != 0) {
-                    dv[1][db] = E::mma(pmv, dot, dv[1][db]);
-                    dk[1][db] = E::mma(dsmv, top(stage, 1, st, cc, db), dk[1][db]);
-                }
+                dv[pw][db] = E::mma(p8, top(stage, 2, st, cc, db), dv[pw][db]);
+                dk[pw][db] = E::mma(ds8, top(stage, pw, st, cc, db), dk[pw][db]);
             }
         }
     };
 
+    // 0 / 1: every pair of the subtile on the self / multimer pathway; 2:
+    // both; 3: nothing to do (no valid query or no valid key).
     auto qmode = [&](int qmin, int qmax, int ninval) {
-        if (ninval == 32) return 3;
-        if (!DENSE && !any_pad) {
+        if (ninval == 32 || !any_live) return 3;
+        if (!DENSE) {
             if (qmin == qmax && kc_min == kc_max && qmin == kc_min) return 0;
             if (qmax < kc_min || qmin > kc_max) return 1;
         }
@@ -683,41 +665,62 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
         if (first + lane < Lp / 32) v = qsum_b[first + lane];
         return v;
     };
+    // vector-memory instructions one issue() puts in flight (uniform)
+    int ncp = 1;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) ncp += (TOT % W == 0 || wave + j * W < TOT) ? 1 : 0;
+    if constexpr (DENSE) {
+        if (a.mdma)
+            for (int m = wave; m < MSK / 1024; m += W) ++ncp;
+    }
     int sub0 = 0;
     int4 qsw = sum_window(0);
-    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // (compiler-visible) the window has landed
+#pragma unroll
+    for (int t = 0; t < NBUF - 1; ++t)
+        if (t < nst) issue(t, t);
+    int bf = 0;
     for (int s = 0; s < nst; ++s) {
-        const int bf = s & 1;
-        // (compiler-visible: every load of the wave has landed here)
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        // stage s's copies have landed (later stages' may stay in flight)
+        if (NBUF == 3 && s + 1 < nst) wait_vm_var(ncp);
+        else wait_vm<0>();
         stage_barrier();
         if (2 * s - sub0 >= 64) {
             sub0 = 2 * s;
             qsw = sum_window(sub0);
-            __builtin_amdgcn_s_waitcnt(0x0F70);  // before the next copy is issued
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // (drains the copies in flight too; rare)
         }
-        if (s + 1 < nst) issue(s + 1, bf ^ 1);
+        if (s + NBUF - 1 < nst) issue(s + NBUF - 1, bf == 0 ? NBUF - 1 : bf - 1);
         const char* stage = smem + bf * STAGE;
         const int q0 = s * kBS;
+        int md2[2];
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
             const int i = 2 * s + st - sub0;
-            const int md = qmode(__builtin_amdgcn_readlane(qsw.x, i), __builtin_amdgcn_readlane(qsw.y, i),
-                                 __builtin_amdgcn_readlane(qsw.z, i));
-            if (md == 0) subtile(stage, st, 0, q0);
-            else if (md == 1) subtile(stage, st, 1, q0);
-            else if (md == 2) subtile(stage, st, 2, q0);
+            md2[st] = qmode(__builtin_amdgcn_readlane(qsw.x, i), __builtin_amdgcn_readlane(qsw.y, i),
+                            __builtin_amdgcn_readlane(qsw.z, i));
         }
+        // Up to two passes per subtile (one per pathway for mixed ones), from
+        // one instance of the pass code.
+#pragma unroll 1
+        for (int it = 0; it < 4; ++it) {
+            const int st = it >> 1, ps = it & 1;
+            const int md = st ? md2[1] : md2[0];
+            if (md == 3 || (ps == 1 && md != 2)) continue;
+            if ((md == 2 ? ps : md) == 0) pass(md == 2, IC<0>{}, stage, st, q0);
+            else pass(md == 2, IC<1>{}, stage, st, q0);
+        }
+        bf = bf + 1 == NBUF ? 0 : bf + 1;
     }
     wait_vm<0>();
     stage_barrier();  // stage buffers become epilogue scratch
 
     float* scratch = (float*)(smem + wave * 32 * 65 * 4);
     const float vmul = DROP ? a.drop.rkeep : 1.0f;
-    store_rows<T, D, false>(dv[0], scratch, p.dv_self, b, h, kw0, L, vmul, false, nullptr, nullptr);
-    store_rows<T, D, false>(dv[1], scratch, p.dv_multi, b, h, kw0, L, vmul, false, nullptr, nullptr);
-    store_rows<T, D, false>(dk[0], scratch, p.dk_self, b, h, kw0, L, a.kmul, ROPE, p.rope_cos, p.rope_sin);
-    store_rows<T, D, false>(dk[1], scratch, p.dk_multi, b, h, kw0, L, a.kmul, false, nullptr, nullptr);
+    store_rows<T, D, false>(dv[0], scratch, p.dv_self, b, h, kw0, L, vmul, false, nullptr, nullptr, key_live);
+    store_rows<T, D, false>(dv[1], scratch, p.dv_multi, b, h, kw0, L, vmul, false, nullptr, nullptr, key_live);
+    store_rows<T, D, false>(dk[0], scratch, p.dk_self, b, h, kw0, L, a.kmul, ROPE, p.rope_cos, p.rope_sin, key_live);
+    store_rows<T, D, false>(dk[1], scratch, p.dk_multi, b, h, kw0, L, a.kmul, false, nullptr, nullptr, key_live);
 }
 
 // ---------------------------------------------------------------------------
