@@ -32,77 +32,17 @@
 //     dP^T = V dO^T and dQ^T += K^T dS^T.
 #include <type_traits>
 
-#include "mpattn_common.h"
+#include "mpattn_bwd.h"
 
 namespace mpattn {
 
-constexpr int kBS = 64;  // rows per LDS stage
-
-static inline int rup(int x, int m) { return (x + m - 1) / m * m; }
-
 template <int N> using IC = std::integral_constant<int, N>;
-
-// Workspace layout (offsets 256-byte aligned), Lp = L rounded up to 64:
-//   lse2  f32   [B][H][Lp]   LSE * log2(e); +inf past L
-//   delta f32   [B][H][Lp]   dO . O; 0 past L
-//   keff  int32 [B][Lp]      key chain id, kPadChain for padded / past L
-//   ksum  int32 [B][Lp/32][4] key blocks: min, max chain (valid keys), #padded
-//   qcid  int32 [B][Lp]      query chain id (queries past L: 0)
-//   qsum  int32 [B][Lp/32][4] query blocks: min, max chain (queries < L)
-//   qrot, krot, qmf T [B][H][Lp][D]  fused RoPE only: the forward's MFMA
-//                operands, rounded as the forward rounds them: Q_self rotated
-//                and multiplied by the logit factor, K_self rotated, Q_multi
-//                multiplied by the logit factor (so the logits recomputed here
-//                are the ones the forward's LSE was taken over)
-struct BwdWs {
-    int64_t lse2, delta, keff, ksum, qcid, qsum, qrot, krot, qmf, total;
-};
-
-static inline BwdWs bwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
-    const int64_t Lp = rup(L, kBS);
-    auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
-    BwdWs w;
-    w.lse2 = 0;
-    w.delta = al(w.lse2 + (int64_t)B * H * Lp * 4);
-    w.keff = al(w.delta + (int64_t)B * H * Lp * 4);
-    w.ksum = al(w.keff + (int64_t)B * Lp * 4);
-    w.qcid = al(w.ksum + (int64_t)B * (Lp / 32) * 16);
-    w.qsum = al(w.qcid + (int64_t)B * Lp * 4);
-    w.qrot = al(w.qsum + (int64_t)B * (Lp / 32) * 16);
-    const int64_t rot = rope ? (int64_t)B * H * Lp * D * esize : 0;
-    w.krot = al(w.qrot + rot);
-    w.qmf = al(w.krot + rot);
-    w.total = al(w.qmf + rot);
-    return w;
-}
 
 int64_t bwd_workspace_bytes(int B, int H, int L, int D) {
     // Sized for the largest element type and fused RoPE: callers allocate
     // once regardless of the mode.
     return bwd_ws_layout(B, H, L, D, 4, true).total;
 }
-
-struct BwdArgs {
-    mpattn_bwd_params p;
-    const float* lse2;
-    const float* delta;
-    const int* keff;
-    const int* ksum;
-    const int* qcid;
-    const int* qsum;
-    const void* qrot;
-    const void* krot;
-    const void* qmf;  // folded Q_multi (fused RoPE)
-    float kmul;       // dK factor: scale, or scale / (logit factor) when Q is folded
-    int Lp;
-    float c;     // logit factor: scale * log2(e), halved for sqrt-softmax (1 when
-                 // fused RoPE folds it into Q, as the forward does)
-    float lmul;  // LSE factor: log2(e), halved for sqrt-softmax
-    float qmul;  // logit factor folded into Q by the prep kernel (fused RoPE)
-    DropCfg drop;
-    int mvec;  // dense mask rows readable as aligned 8-byte words
-    int mdma;  // dense mask tiles copyable to LDS in 16-byte chunks (dK/dV)
-};
 
 // ---------------------------------------------------------------------------
 // Prep: chain staging, Delta / LSE2 rows, RoPE of Q_self and K_self.
@@ -1089,11 +1029,14 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     // With fused RoPE the forward folds the logit factor into Q (both
     // pathways); the backward recomputes the logits from the same folded,
     // rounded operands (prep kernel), so c = 1 and dK = (scale / f) dS^T Qf.
-    const float f = p.scale * kLog2e * (SQRT ? 0.5f : 1.0f);
+    // The fp32 forward takes sqrt-softmax as the square root of the full
+    // softmax (logit factor not halved), and so does the fp32 backward.
+    constexpr bool F32 = std::is_same<T, float>::value;
+    const float f = p.scale * kLog2e * (SQRT && !F32 ? 0.5f : 1.0f);
     a.c = ROPE ? 1.0f : f;
     a.qmul = f;
     a.kmul = ROPE ? p.scale / f : p.scale;
-    a.lmul = kLog2e * (SQRT ? 0.5f : 1.0f);
+    a.lmul = kLog2e * (SQRT && !F32 ? 0.5f : 1.0f);
     a.drop = drop_cfg(p.dropout_p, p.dropout_seed);
     a.mvec = p.chain_mask && p.mask_stride_k == 1 && (uintptr_t)p.chain_mask % 8 == 0 && p.mask_stride_b % 8 == 0 &&
              p.mask_stride_q % 8 == 0;
@@ -1126,12 +1069,16 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
                        a, lse2, delta, keff, ksum, qcid, qsum, qrot, krot, qmf, nchain, nrow);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if constexpr (F32) {
+        return launch_bwd32(a, stream);
+    } else {
     const int nb = (p.L + 32 * W - 1) / (32 * W);
     const unsigned grid = (unsigned)((int64_t)p.B * p.H * nb);
     hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(grid), dim3(W * 64), 0, stream, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(grid), dim3(W * 64), 0, stream, a);
     return hipGetLastError();
+    }
 }
 
 template <typename T, int D>
@@ -1142,7 +1089,7 @@ static hipError_t dispatch_bwd_d(const mpattn_bwd_params& p, hipStream_t s) {
         if (rope) return dense ? launch_bwd_t<T, D, true, true, true, false>(p, s) : launch_bwd_t<T, D, true, false, true, false>(p, s);
         return dense ? launch_bwd_t<T, D, false, true, true, false>(p, s) : launch_bwd_t<T, D, false, false, true, false>(p, s);
     }
-    if (p.dropout_p > 0.f) {
+    if (p.dropout_p > 0.f && !std::is_same<T, float>::value) {  // (no fp32 dropout: rejected by the API)
         if (rope) return dense ? launch_bwd_t<T, D, true, true, false, true>(p, s) : launch_bwd_t<T, D, true, false, false, true>(p, s);
         return dense ? launch_bwd_t<T, D, false, true, false, true>(p, s) : launch_bwd_t<T, D, false, false, false, true>(p, s);
     }
@@ -1162,7 +1109,7 @@ static hipError_t dispatch_bwd_t(const mpattn_bwd_params& p, hipStream_t s) {
 }
 
 hipError_t launch_bwd(const mpattn_bwd_params& p, hipStream_t stream) {
-    if (p.dtype == MPATTN_FP32) return hipErrorInvalidValue;  // not built
+    if (p.dtype == MPATTN_FP32) return dispatch_bwd_t<float>(p, stream);
     if (p.dtype == MPATTN_BF16) return dispatch_bwd_t<bf16_t>(p, stream);
     return dispatch_bwd_t<fp16_t>(p, stream);
 }

@@ -66,6 +66,13 @@ template <> struct Elt<fp16_t> {
     }
 };
 
+// fp32 rows, for the kernels that handle every element type alike (the
+// backward's prep: Delta, LSE2 and the RoPE-rotated operands).
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+template <> struct Elt<float> {
+    typedef f32x8 v8;
+};
+
 __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);
 }

@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void fwd32_kernel(const mpattn_fwd_params p, c
                 const int fi = lo ? d : d - H2;
                 const float y = row[lo ? d + H2 : d - H2];
                 const float cs = p.rope_cos[(int64_t)q * H2 + fi], sn = p.rope_sin[(int64_t)q * H2 + fi];
-                x = lo ? x * cs - y * sn : x * cs + y * sn;
+                x = rope_rot(x, y, cs, sn, lo);
             }
             qf[pw][kk] = x * qmul;
         }
@@ -125,11 +125,10 @@ __global__ __launch_bounds__(256) void fwd32_kernel(const mpattn_fwd_params p, c
                 const float4 y = *reinterpret_cast<const float4*>(rowp + (lo ? d0 + H2 : d0 - H2));
                 const float4 cs = *reinterpret_cast<const float4*>(p.rope_cos + (int64_t)key * H2 + fi);
                 const float4 sn = *reinterpret_cast<const float4*>(p.rope_sin + (int64_t)key * H2 + fi);
-                const float sg = lo ? -1.f : 1.f;
-                x.x = x.x * cs.x + sg * y.x * sn.x;
-                x.y = x.y * cs.y + sg * y.y * sn.y;
-                x.z = x.z * cs.z + sg * y.z * sn.z;
-                x.w = x.w * cs.w + sg * y.w * sn.w;
+                x.x = rope_rot(x.x, y.x, cs.x, sn.x, lo);
+                x.y = rope_rot(x.y, y.y, cs.y, sn.y, lo);
+                x.z = rope_rot(x.z, y.z, cs.z, sn.z, lo);
+                x.w = rope_rot(x.w, y.w, cs.w, sn.w, lo);
             }
             float* dst = st + ten * TILE + r * RS + d0;
             dst[0] = x.x;

@@ -169,14 +169,12 @@ class TransformerLayer_MINT(nn.Module):
         return self.self_attn.out_proj(out).transpose(0, 1).contiguous(), None
 
     def _fused_covers(self, x):
-        """The fused kernels serve 16-bit inputs in training and inference,
-        fp32 inputs for inference without dropout (the fp32 fused backward
-        and fp32 dropout are not built; the combine kernels cover them)."""
+        """The fused kernels serve 16-bit inputs in every mode and fp32
+        inputs in every mode but training with dropout (fp32 dropout is not
+        built; the combine kernels cover it)."""
         if x.dtype != torch.float32:
             return True
-        sa, ma = self.self_attn, self.multimer_attn
-        grad = torch.is_grad_enabled() and (x.requires_grad or _needs_grad(sa, ma))
-        return not grad and not (self.training and sa.dropout > 0)
+        return not (self.training and self.self_attn.dropout > 0)
 
     def _multimer_attention_plus(self, x, chain_mask, padding_mask, chain_ids=None):
         """Dispatch (modules.py:200-249): fused multi-pathway kernel when the

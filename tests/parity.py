@@ -197,6 +197,71 @@ def assert_grads16(got, ref, what):
     assert not bad, f"{what}: " + "; ".join(f"{n}: {m}" for n, m in bad)
 
 
+# fp32 bound (the task's fp32 tolerance): max |gpu - ref| <= 1e-4 and
+# ||gpu - ref||_F <= 1e-4 ||ref||_F per tensor.
+ATOL32, RELF32 = 1e-4, 1e-4
+
+
+def compare32(got, ref):
+    """Both fp32 bounds for one tensor; returns None if they hold, else a message."""
+    g, r = _as_np(got), _as_np(ref)
+    if g.shape != r.shape:
+        return f"shape {g.shape} != {r.shape}"
+    if not np.isfinite(g).all():
+        return f"{int((~np.isfinite(g)).sum())} non-finite elements"
+    err = float(np.abs(g - r).max()) if g.size else 0.0
+    nr = float(np.linalg.norm(r))
+    rel = float(np.linalg.norm(g - r)) / nr if nr > 0 else float(np.linalg.norm(g))
+    msgs = []
+    if err > ATOL32:
+        msgs.append(f"max err {err:.3g} > {ATOL32}")
+    if rel > RELF32:
+        msgs.append(f"relative Frobenius error {rel:.3g} > {RELF32}")
+    return "; ".join(msgs) or None
+
+
+def compare_grads32(got, ref):
+    out = []
+    for n, g, r in zip(GRAD_NAMES, got, ref):
+        m = compare32(g, r)
+        if m:
+            out.append((n, m))
+    return out
+
+
+def assert_grads32(got, ref, what):
+    bad = compare_grads32(got, ref)
+    assert not bad, f"{what}: " + "; ".join(f"{n}: {m}" for n, m in bad)
+
+
+def bwd32_inputs(B, H, L, D, seed, scale, rope=True, sigma=1.0, nchains=2, pad=True,
+                 sqrt_softmax=False, dense=False):
+    """fp32 backward case: Q/K entries N(0, sigma^2), V N(0, 1) (logit std
+    about sigma^2 * sqrt(D) * scale), chain ids and key padding, and an
+    upstream gradient N(0, 1) times the power of two that brings the largest
+    oracle gradient RMS into [0.7, 1.4] (gradients are linear in dO, so the
+    oracle's gradients are scaled by the same exact factor).
+
+    Returns (xs, go, cid, kp, ref) with float32 numpy inputs and the float64
+    oracle gradients."""
+    from oracle import mpattn_oracle as orc
+    rng = np.random.default_rng(seed)
+    z = [rng.standard_normal((B, H, L, D)).astype(np.float32) for _ in range(6)]
+    mul = [sigma, sigma, 1.0, sigma, sigma, 1.0]
+    xs = [(x * np.float32(m)).astype(np.float32) for x, m in zip(z, mul)]
+    cid = chains(rng, B, L, nchains)
+    kp = tail_padding(rng, B, L) if pad else np.zeros((B, L), dtype=bool)
+    go = rng.standard_normal((B, H, L, D)).astype(np.float32)
+    sel = dict(chain_mask=(cid[:, :, None] != cid[:, None, :])) if dense else dict(chain_ids=cid)
+    ref = orc.mpattn_backward(*[x.astype(np.float64) for x in xs], go.astype(np.float64), key_pad=kp,
+                              rope=rope, scale=scale, sqrt_softmax=sqrt_softmax, **sel)
+    rms = max(float(np.sqrt(np.mean(r ** 2))) for r in ref)
+    f = 2.0 ** -round(np.log2(rms)) if rms > 0 else 1.0
+    go = (go * np.float32(f)).astype(np.float32)
+    ref = [r * f for r in ref]
+    return xs, go, cid, kp, ref
+
+
 def round_operands(xs, D, scale, rope, dtype):
     """The operands the 16-bit kernels feed their MFMAs: with fused RoPE, Q
     is rotated and multiplied by scale*log2(e) in fp32 and rounded once

@@ -96,15 +96,21 @@ def test_layer_bf16_fused(E, H):
 
 @pytest.mark.parametrize("fused,dtype", [(True, torch.bfloat16), (False, torch.float32),
                                          (True, torch.float32)])
-def test_layer_backward_matches_eager(fused, dtype):
+def test_layer_backward_matches_eager(fused, dtype, monkeypatch):
     """Training step through the HIP path: input and parameter gradients of
     the GPU layer against torch autograd of the same layer's eager path in
     float64 on the CPU (itself pinned to the layer oracle on the CPU).
-    Fused path, bf16 layer: bound 2e-2 of each gradient's max; combine path,
-    fp32 layer: bound 1e-4 of each max. An fp32 layer with the fused flag
-    trains through the combine kernels (no fp32 fused backward is built)."""
+    bf16 layer (fused kernels): bound 2e-2 of each gradient's max; fp32
+    layer (the 8M width; fused fp32 forward and backward, or the combine
+    kernels): bound 1e-4 of each max. With the fused flag the combine
+    kernels must not run."""
     print(f"[layer bwd] fused={fused} dtype={dtype}", flush=True)
     M, _, _ = _mods()
+    if fused:
+        def no_combine(*a, **k):
+            raise AssertionError("combine kernels called on the fused path")
+        monkeypatch.setattr(M, "differentiable_multimer_combine", no_combine)
+        monkeypatch.setattr(M, "fused_multimer_combine", no_combine)
     torch.manual_seed(15)
     T, B, E, H = 130, 2, 320, 20
     ref_layer = M.TransformerLayer_MINT(E, 2 * E, H, use_multimer=True).double().train()

@@ -8,7 +8,8 @@ the same comparison (``tests/parity.py``) on CPU oracle results and checks:
   pathways, one 256-query block zeroed, dropped RoPE (cases whose logits
   RoPE moves by O(1)); for the backward, each of dQ/dK of either pathway
   zeroed, dQ and dK swapped, dQ and dK halved, swapped pathways, one
-  256-query block of dQ_self zeroed, dropped RoPE;
+  256-query block of dQ_self zeroed, dropped RoPE; the same for the fp32
+  backward cases of ``tests/test_bwd32_gpu.py`` at the fp32 bound;
 * the comparison accepts the oracle evaluated on the operands rounded as
   the kernels round them (fused RoPE: rotated Q and K rounded to the input
   dtype), so a correct kernel is not rejected by the rounding of its
@@ -26,6 +27,7 @@ import pytest
 import torch
 
 import parity as P
+import test_bwd32_gpu as BW32
 import test_bwd_gpu as BW
 import test_fwd_gpu as FW
 from oracle import mpattn_oracle as orc
@@ -257,3 +259,107 @@ def test_power_detects_planted_oracle_rope_mistake():
     bad = P.ref_forward(a, cid, kp, False, 32 ** -0.5)
     assert P.compare16(bad, ref) is not None
     assert np.isfinite(ref).all()
+
+
+# ---------------------------------------------------------------- fp32 backward
+
+def _grads32_autograd(xs, go, cid, kp, rope, scale, sqrt_softmax, dense, dtype):
+    """Gradients of sum(out * go) by torch autograd through ``torch_ref`` in
+    ``dtype`` (float32: a correct fp32 implementation's arithmetic)."""
+    leaves = [torch.from_numpy(x).to(dtype).requires_grad_(True) for x in xs]
+    sel = {}
+    if dense:
+        c = torch.from_numpy(cid)
+        sel["chain_mask"] = c[:, :, None] != c[:, None, :]
+    else:
+        sel["chain_ids"] = torch.from_numpy(cid)
+    if sqrt_softmax:
+        # sqrt(P) as exp((s - LSE) / 2): autograd through sqrt would give
+        # 0 * inf at the padded keys (torch_ref is a forward reference)
+        qs, ks, vs, qm, km, vm = leaves
+        if rope:
+            cos, sin = torch_ref.rope_tables(xs[0].shape[2], xs[0].shape[3], "cpu", dtype)
+            qs, ks = torch_ref.apply_rope(qs, cos, sin), torch_ref.apply_rope(ks, cos, sin)
+        c = sel.get("chain_mask")
+        if c is None:
+            ci = sel["chain_ids"]
+            c = ci[:, :, None] != ci[:, None, :]
+        c = c[:, None]
+        sc = torch.where(c, scale * qm @ km.transpose(-1, -2), scale * qs @ ks.transpose(-1, -2))
+        sc = sc.masked_fill(torch.from_numpy(kp)[:, None, None, :], float("-inf"))
+        w = torch.exp(0.5 * (sc - torch.logsumexp(sc, dim=-1, keepdim=True)))
+        out = w.masked_fill(c, 0.0) @ vs + w.masked_fill(~c, 0.0) @ vm
+    else:
+        out, _ = torch_ref.forward(*leaves, key_pad=torch.from_numpy(kp), rope=rope, scale=scale,
+                                   dtype=dtype, chunk=1, **sel)
+    (out * torch.from_numpy(go).to(dtype)).sum().backward()
+    return [leaf.grad.double().numpy() for leaf in leaves]
+
+
+def check_bwd32_case(case, rope, scale, sqrt_softmax=False, dense=False):
+    """The fp32 GPU comparison (``parity.compare_grads32``) accepts fp32
+    autograd of the reference forward with margin (at most 1/4 of each
+    bound) and rejects the planted mistakes."""
+    xs, go, cid, kp, ref = case
+    B, H, L, D = xs[0].shape
+    f32 = _grads32_autograd(xs, go, cid, kp, rope, scale, sqrt_softmax, dense, torch.float32)
+    for n, g, r in zip(P.GRAD_NAMES, f32, ref):
+        err = float(np.abs(g - r).max())
+        nr = float(np.linalg.norm(r))
+        rel = float(np.linalg.norm(g - r)) / nr if nr > 0 else float(np.linalg.norm(g))
+        assert err <= P.ATOL32 / 4 and rel <= P.RELF32 / 4, (n, err, rel)
+    names = P.GRAD_NAMES
+    cands = {}
+    for i in (0, 1, 3, 4):
+        if np.any(ref[i] != 0):
+            g = list(ref)
+            g[i] = g[i] * 0
+            cands[f"zero_{names[i]}"] = g
+    g = list(ref)
+    g[0], g[1], g[3], g[4] = ref[1], ref[0], ref[4], ref[3]
+    cands["swap_dq_dk"] = g
+    g = list(ref)
+    for i in (0, 1, 3, 4):
+        g[i] = g[i] * 0.5
+    cands["half_dq_dk"] = g
+    g = list(ref)
+    g[0], g[1], g[2], g[3], g[4], g[5] = ref[3], ref[4], ref[5], ref[0], ref[1], ref[2]
+    cands["swap_pathways"] = g
+    g = list(ref)
+    blk = ref[0].copy()
+    b, h, qs = _block(B, H, L)
+    blk[b, h, qs] = 0
+    g[0] = blk
+    cands["block_dq_self"] = g
+    if rope:
+        sel = dict(chain_mask=(cid[:, :, None] != cid[:, None, :])) if dense else dict(chain_ids=cid)
+        cands["no_rope"] = orc.mpattn_backward(*[x.astype(np.float64) for x in xs], go.astype(np.float64),
+                                               key_pad=kp, rope=False, scale=scale,
+                                               sqrt_softmax=sqrt_softmax, **sel)
+    passed = [k for k, v in cands.items() if not P.compare_grads32(v, ref)]
+    assert not passed, f"planted mistakes not rejected: {passed}"
+
+
+@pytest.mark.parametrize("D,L", BW32.SMALL)
+def test_power_bwd32_small(D, L):
+    check_bwd32_case(BW32.small_case(D, L), True, D ** -0.5)
+
+
+@pytest.mark.parametrize("n", BW32.CHAIN_COUNTS)
+def test_power_bwd32_chains(n):
+    check_bwd32_case(BW32.chain_case(n), True, 0.25)
+
+
+@pytest.mark.parametrize("D", [32, 64])
+def test_power_bwd32_dense(D):
+    check_bwd32_case(BW32.dense_case(D), False, 1.0, dense=True)
+
+
+@pytest.mark.parametrize("D", [16, 32])
+def test_power_bwd32_sqrt(D):
+    check_bwd32_case(BW32.sqrt_case(D), True, D ** -0.5, sqrt_softmax=True)
+
+
+def test_power_bwd32_long_rows():
+    B, H, L, D, n = BW32.LARGE[2]
+    check_bwd32_case(BW32.large_case(B, H, L, D, n), True, D ** -0.5)
