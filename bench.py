@@ -34,9 +34,11 @@ B, H, L, D = 16, 20, 1024, 32
 SEED = 150
 
 
-def make_workload(device, seed=SEED):
+def make_workload(device, seed=SEED, d=D, dtype=torch.bfloat16):
+    """The headline batch; ``d`` / ``dtype`` give the same
+    batch at another head dim or element type (per-head-dim modes)."""
     g = torch.Generator(device="cpu").manual_seed(seed)
-    xs = [(torch.randn(B, H, L, D, generator=g) / D ** 0.5).to(torch.bfloat16).to(device)
+    xs = [(torch.randn(B, H, L, d, generator=g) / d ** 0.5).to(dtype).to(device)
           for _ in range(6)]
     cid = torch.zeros(B, L, dtype=torch.int32)
     pad = torch.zeros(B, L, dtype=torch.bool)
@@ -135,10 +137,12 @@ def model_batch(device, seed, B, lo, hi, min_chain):
 
 
 def bench_model(dev, size="650M", dtype=torch.bfloat16, B=8, steps=5, warmup=2,
-                paths=("fused", "combine", "eager")):
+                paths=("fused", "combine", "eager", "eager_reference")):
     """Full MINT forward (embedding extraction) with random-init weights:
     seconds per forward and sequences/s for each multimer-attention path:
-    fused HIP kernel, materialised logits + HIP combine kernel, eager torch."""
+    fused HIP kernel, materialised logits + HIP combine kernel, eager torch
+    with an fp32 softmax ("eager") and eager torch with the reference's bf16
+    softmax arithmetic ("eager_reference", modules_plus.py:182-194)."""
     from mint_plus_amd import esm2, modules
     torch.manual_seed(65)
     with torch.device(dev):
@@ -150,7 +154,7 @@ def bench_model(dev, size="650M", dtype=torch.bfloat16, B=8, steps=5, warmup=2,
            "tokens": int((tok != 1).sum()), "dtype": str(dtype).replace("torch.", "")}
     for path in paths:
         modules.enable_fused_multi_pathway(model, path == "fused")
-        modules.use_eager_multimer(model, path == "eager")
+        modules.use_eager_multimer(model, "reference" if path == "eager_reference" else path == "eager")
 
         def step():
             with torch.inference_mode():
@@ -160,8 +164,9 @@ def bench_model(dev, size="650M", dtype=torch.bfloat16, B=8, steps=5, warmup=2,
         ms = statistics.median(per)
         out[f"ms_fwd_{path}"] = round(ms, 3)
         out[f"seqs_per_sec_{path}"] = round(B / (ms * 1e-3), 2)
-    if "fused" in paths and "eager" in paths:
-        out["speedup_fused_vs_eager"] = round(out["ms_fwd_eager"] / out["ms_fwd_fused"], 3)
+    for e in ("eager", "eager_reference"):
+        if "fused" in paths and e in paths:
+            out[f"speedup_fused_vs_{e}"] = round(out[f"ms_fwd_{e}"] / out["ms_fwd_fused"], 3)
     del model
     torch.cuda.empty_cache()
     return out
@@ -173,14 +178,20 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--mode", choices=("fwd", "fwdbwd", "model", "attn3b", "attn650m", "combine", "dense"),
+    ap.add_argument("--mode", choices=("fwd", "fwdbwd", "model", "attn3b", "attn650m", "combine", "dense",
+                                       "headdim", "attn8m"),
                     default="fwd",
                     help="fwd: the headline forward (B=16); fwdbwd: forward + backward at the "
                          "training shape (B=8, dO ~ N(0, 1)); model: 650M MINT forward "
                          "sequences/s per attention path; attn3b / attn650m: the op at the 3B / "
                          "650M model's attention shape; dense: the 150M forward through the "
                          "reference's (B, L, L) chain-mask contract; "
-                         "combine: the materialised-logit combine fwd and bwd (HBM-bound)")
+                         "combine: the materialised-logit combine fwd and bwd (HBM-bound); "
+                         "headdim: the headline batch at D = 16, 24, 32, 64 (one line each, "
+                         "forward and forward+backward; --dtype); attn8m: fp32 forward and "
+                         "forward+backward at the 8M model's attention shape (configs[0])")
+    ap.add_argument("--dtype", choices=("bf16", "fp32"), default="bf16",
+                    help="element type of --mode headdim")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the 650M model forward summary of the default line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -224,6 +235,10 @@ def main():
         return bench_combine(args, dev)
     if args.mode == "dense":
         return bench_dense(args, dev)
+    if args.mode == "headdim":
+        return bench_headdim(args, dev)
+    if args.mode == "attn8m":
+        return bench_attn8m(args, dev)
     xs, cid, pad = make_workload(dev)
     out = torch.empty_like(xs[0])
 
@@ -280,7 +295,7 @@ def main():
     }
     if not args.no_model:
         # 650M full-model forward, sequences/s: fused HIP path vs eager attention
-        res["model_650m_fwd"] = bench_model(dev, paths=("fused", "eager"))
+        res["model_650m_fwd"] = bench_model(dev, paths=("fused", "eager", "eager_reference"))
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)
@@ -429,6 +444,85 @@ def bench_attn_shape(args, dev, shape):
                       "p90": round(per[(9 * len(per)) // 10], 5)},
         "pct_bf16_peak": round(100.0 * fl / (med * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
     }), flush=True)
+
+
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA
+
+
+def _fwd_fwdbwd_lines(args, dev, xs, cid, pad, d, dtype_name, peak, metric, config, data):
+    """Time the forward and the forward+backward of the op on these inputs
+    (fused RoPE, scale d^-1/2, dO ~ N(0, 1)); print one JSON line."""
+    from mint_plus_amd import _lib
+    b, h, l = xs[0].shape[:3]
+    sel = dict(chain_ids=cid, key_padding_mask=pad, rope=True, scale=d ** -0.5)
+    out = torch.empty_like(xs[0])
+    g = torch.Generator(device="cpu").manual_seed(SEED + 2)
+    go = torch.randn(xs[0].shape, generator=g).to(xs[0].dtype).to(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def fwd():
+        _lib.mpattn_fwd(*xs, out=out, **sel)
+
+    def fwdbwd():
+        _, lse = _lib.mpattn_fwd(*xs, need_lse=True, out=out, **sel)
+        _lib.mpattn_bwd(*xs, out, lse, go, **sel)
+
+    ffl = 4.0 * b * h * l * l * d
+    res = {"metric": metric, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "higher_is_better": True, "dtype": dtype_name, "data": data,
+           "config": dict(config, B=b, H=h, L=l, D=d, rope="fused")}
+    for name, fn, fl in (("fwd", fwd, ffl), ("fwdbwd", fwdbwd, 3.0 * ffl)):
+        wall, per = timed(fn, args.steps, args.warmup, stream)
+        med = statistics.median(per)
+        mean_ms = sum(per) / len(per)
+        res[f"{name}_ms"] = {"median": round(med, 5), "p10": round(per[len(per) // 10], 5),
+                             "p90": round(per[(9 * len(per)) // 10], 5), "mean": round(mean_ms, 5)}
+        res[f"{name}_tflops"] = round(fl / (med * 1e-3) / 1e12, 2)
+        res[f"{name}_frac_peak"] = round(fl / (mean_ms * 1e-3) / 1e12 / peak, 4)
+        if name == "fwd":
+            res["ms_per_step"] = round(wall * 1e3 / args.steps, 5)
+    res["value"] = res["fwd_tflops"]
+    res["peak_tflops"] = peak
+    print(json.dumps(res), flush=True)
+
+
+def bench_headdim(args, dev):
+    """The headline batch (B=16, H=20, L=1024, two chains, pad tail) at each
+    head dim of the ESM-2 family (8M: 16, 35M: 24, 150M: 32, 650M/3B: 64),
+    in bf16 or fp32. Algorithmic flops: forward 4*B*H*L^2*D, backward twice
+    that (fwd+bwd 12*B*H*L^2*D; the backward's recompute is not counted)."""
+    bf = args.dtype == "bf16"
+    dt = torch.bfloat16 if bf else torch.float32
+    peak = PEAK_BF16_TFLOPS if bf else PEAK_FP32_TFLOPS
+    for d in (16, 24, 32, 64):
+        xs, cid, pad = make_workload(dev, d=d, dtype=dt)
+        _fwd_fwdbwd_lines(args, dev, xs, cid, pad, d, args.dtype, peak,
+                          f"multi-pathway attn TFLOP/s (150M batch, D={d}, {args.dtype})",
+                          {"workload": f"headline batch at head dim {d}", "chains": 2},
+                          f"synthetic (seeded N(0,1)/sqrt({d}) projections, 2 chains, 0-10% pad tail)")
+        del xs
+        torch.cuda.empty_cache()
+
+
+def bench_attn8m(args, dev):
+    """The op in fp32 at the ESM-2 8M MINT model's attention shape
+    (configs[0]): B=4, H=20, D=16, two chains of U[60,200] + U[40,160]
+    residues plus <cls>/<eos> each, padded to the batch max."""
+    g = torch.Generator(device="cpu").manual_seed(8)
+    b, h, d = 4, 20, 16
+    la = [int(torch.randint(60, 201, (1,), generator=g)) + 2 for _ in range(b)]
+    lb = [int(torch.randint(40, 161, (1,), generator=g)) + 2 for _ in range(b)]
+    l = max(x + y for x, y in zip(la, lb))
+    cid = torch.zeros(b, l, dtype=torch.int32)
+    pad = torch.zeros(b, l, dtype=torch.bool)
+    for i in range(b):
+        cid[i, la[i]:] = 1
+        pad[i, la[i] + lb[i]:] = True
+    xs = [(torch.randn(b, h, l, d, generator=g) / d ** 0.5).to(dev) for _ in range(6)]
+    _fwd_fwdbwd_lines(args, dev, xs, cid.to(dev), pad.to(dev), d, "fp32", PEAK_FP32_TFLOPS,
+                      "multi-pathway attn TFLOP/s (8M attention shape, fp32)",
+                      {"workload": "8M MINT attention (configs[0]), one layer", "chains": 2},
+                      "synthetic (seeded N(0,1)/4 projections, chains U[60,200]+2 and U[40,160]+2)")
 
 
 def bench_dense(args, dev):

@@ -168,6 +168,27 @@ class TransformerLayer_MINT(nn.Module):
         out = out.transpose(1, 2).reshape(B, T, E)
         return self.self_attn.out_proj(out).transpose(0, 1).contiguous(), None
 
+    def _multimer_attention_reference_arith(self, x, chain_mask, padding_mask, chain_ids=None):
+        """The eager combine with the reference's own arithmetic
+        (modules_plus.py:182-194, modules.py:135-147): softmax returned in
+        bf16 (``dtype=torch.bfloat16``), no ``nan_to_num``, the pathway masks
+        applied to the bf16 probabilities. Kept as the timing baseline of
+        bf16 models; a row whose keys are all padded gives NaN, as in the
+        reference."""
+        T, B, E = x.shape
+        if chain_mask is None:
+            cid, _ = self._selection(None, chain_ids, x)
+            chain_mask = cid[:, :, None] != cid[:, None, :]
+        intra_logits, intra_v = self.self_attn(x=x, key_padding_mask=padding_mask, before_softmax=True)
+        inter_logits, inter_v = self.multimer_attn(x=x, key_padding_mask=padding_mask, before_softmax=True)
+        cross = chain_mask.to(torch.bool).unsqueeze(1)
+        probs = F.softmax(torch.where(cross, inter_logits, intra_logits), dim=-1, dtype=torch.bfloat16)
+        probs = F.dropout(probs, p=self.self_attn.dropout, training=self.training)
+        out = torch.matmul(probs.masked_fill(cross, 0.0), intra_v) + \
+            torch.matmul(probs.masked_fill(~cross, 0.0), inter_v)
+        out = out.transpose(1, 2).reshape(B, T, E)
+        return self.self_attn.out_proj(out).transpose(0, 1).contiguous(), None
+
     def _fused_covers(self, x):
         """The fused kernels serve 16-bit inputs in every mode and fp32
         inputs in every mode but training with dropout (fp32 dropout is not
@@ -182,7 +203,10 @@ class TransformerLayer_MINT(nn.Module):
         pipeline with the combine kernel."""
         if self._use_fused_multi_pathway and self._fused_covers(x):
             return self._multimer_attention_superfused(x, chain_mask, padding_mask, chain_ids)
-        if getattr(self, "_use_eager_multimer", False):
+        eager = getattr(self, "_use_eager_multimer", False)
+        if eager == "reference":
+            return self._multimer_attention_reference_arith(x, chain_mask, padding_mask, chain_ids)
+        if eager:
             return self._multimer_attention(x, chain_mask, padding_mask, chain_ids)
         T, B, E = x.shape
         sa, ma = self.self_attn, self.multimer_attn
@@ -237,10 +261,14 @@ def enable_fused_multi_pathway(model: nn.Module, enabled: bool = True):
             sub._use_fused_multi_pathway = enabled
 
 
-def use_eager_multimer(model: nn.Module, enabled: bool = True):
+def use_eager_multimer(model: nn.Module, enabled=True):
     """Route every layer's non-fused multimer attention through the eager
-    torch combine (``_multimer_attention``, modules.py:94-154) instead of the
-    combine kernel: the baseline the fused path is measured against."""
+    torch combine instead of the combine kernel: the baselines the fused
+    path is measured against. ``True``: ``_multimer_attention`` (fp32
+    softmax, modules.py:94-154); ``"reference"``: the reference's bf16
+    arithmetic (``_multimer_attention_reference_arith``); ``False``: off."""
+    if enabled not in (True, False, "reference"):
+        raise ValueError(f"enabled must be True, False or 'reference' (got {enabled!r})")
     for layer in model.layers:
         for sub in (layer.layers if hasattr(layer, "layers") else (layer,)):
             sub._use_eager_multimer = enabled

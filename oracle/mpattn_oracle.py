@@ -102,6 +102,17 @@ def cross_mask(chain_ids=None, chain_mask=None):
     return c[:, :, None] != c[:, None, :]
 
 
+def _tr(x):
+    """Swap the last two axes."""
+    return np.swapaxes(x, -1, -2)
+
+
+def _mm(a, b):
+    """Batched float64 matrix product over the leading axes (numpy's matmul,
+    BLAS per (b, h) slice)."""
+    return np.matmul(np.ascontiguousarray(a), np.ascontiguousarray(b))
+
+
 def _prepare(qs, ks, qm, km, rope, scale):
     qs, ks, qm, km = (np.asarray(a, dtype=np.float64) for a in (qs, ks, qm, km))
     L, D = qs.shape[-2], qs.shape[-1]
@@ -111,8 +122,8 @@ def _prepare(qs, ks, qm, km, rope, scale):
     else:
         cos = sin = None
         qs_r, ks_r = qs, ks
-    s_self = scale * np.einsum("bhid,bhjd->bhij", qs_r, ks_r)
-    s_multi = scale * np.einsum("bhid,bhjd->bhij", qm, km)
+    s_self = scale * _mm(qs_r, _tr(ks_r))
+    s_multi = scale * _mm(qm, _tr(km))
     return qs_r, ks_r, s_self, s_multi, cos, sin
 
 
@@ -193,8 +204,7 @@ def mpattn_forward(qs, ks, vs, qm, km, vm, chain_ids=None, chain_mask=None, key_
         w = w * z
     c = cross[:, None]
     vs, vm = np.asarray(vs, np.float64), np.asarray(vm, np.float64)
-    out = np.einsum("bhij,bhjd->bhid", np.where(c, 0.0, w), vs) + \
-        np.einsum("bhij,bhjd->bhid", np.where(c, w, 0.0), vm)
+    out = _mm(np.where(c, 0.0, w), vs) + _mm(np.where(c, w, 0.0), vm)
     return out, lse
 
 
@@ -214,10 +224,10 @@ def mpattn_backward(qs, ks, vs, qm, km, vm, grad_out, chain_ids=None, chain_mask
     z = _dropout_factor(np.shape(qs), dropout_p, dropout_seed)
     wz = w if z is None else w * z  # the weights that multiply V
     w_s, w_m = np.where(c, 0.0, wz), np.where(c, wz, 0.0)
-    dv_s = np.einsum("bhij,bhid->bhjd", w_s, g)
-    dv_m = np.einsum("bhij,bhid->bhjd", w_m, g)
+    dv_s = _mm(_tr(w_s), g)
+    dv_m = _mm(_tr(w_m), g)
     # dW_ij = dO_i . V_sel(ij), j, through the dropout factor
-    dw = np.where(c, np.einsum("bhid,bhjd->bhij", g, vm), np.einsum("bhid,bhjd->bhij", g, vs))
+    dw = np.where(c, _mm(g, _tr(vm)), _mm(g, _tr(vs)))
     if z is not None:
         dw = dw * z
     if sqrt_softmax:
@@ -227,10 +237,10 @@ def mpattn_backward(qs, ks, vs, qm, km, vm, grad_out, chain_ids=None, chain_mask
         pdp = p * dw
     ds = pdp - p * pdp.sum(axis=-1, keepdims=True)
     ds_s, ds_m = np.where(c, 0.0, ds), np.where(c, ds, 0.0)
-    dq_s = scale * np.einsum("bhij,bhjd->bhid", ds_s, ks_r)
-    dk_s = scale * np.einsum("bhij,bhid->bhjd", ds_s, qs_r)
-    dq_m = scale * np.einsum("bhij,bhjd->bhid", ds_m, km)
-    dk_m = scale * np.einsum("bhij,bhid->bhjd", ds_m, qm)
+    dq_s = scale * _mm(ds_s, ks_r)
+    dk_s = scale * _mm(_tr(ds_s), qs_r)
+    dq_m = scale * _mm(ds_m, km)
+    dk_m = scale * _mm(_tr(ds_m), qm)
     if rope:
         dq_s = apply_rope_transpose(dq_s, cos, sin)
         dk_s = apply_rope_transpose(dk_s, cos, sin)
@@ -274,7 +284,7 @@ def combine_backward(intra_logits, inter_logits, chain_mask, vs, vm, grad_out, d
     pz = p if z is None else p * z
     d_vs = np.einsum("bhij,bhid->bhjd", np.where(c, 0.0, pz), g)
     d_vm = np.einsum("bhij,bhid->bhjd", np.where(c, pz, 0.0), g)
-    dw = np.where(c, np.einsum("bhid,bhjd->bhij", g, vm), np.einsum("bhid,bhjd->bhij", g, vs))
+    dw = np.where(c, _mm(g, _tr(vm)), _mm(g, _tr(vs)))
     if z is not None:
         dw = dw * z
     pdp = p * dw

@@ -150,6 +150,39 @@ def test_eager_combine_path_matches_layer_oracle(plus):
     torch.testing.assert_close(y, ref, rtol=0, atol=1e-10)
 
 
+def test_reference_arithmetic_eager_path():
+    """The eager path with the reference's bf16 softmax arithmetic (the
+    650M timing baseline): a bf16 layer's attention output agrees with the
+    float64 eager path on the same bf16 weights to bf16 accuracy; all-padded
+    rows give NaN (the reference applies no nan_to_num); the switch accepts
+    only True, False and "reference"."""
+    torch.manual_seed(4)
+    T, B, E, H = 48, 2, 64, 4
+    layer = M.TransformerLayer_MINT(E, 2 * E, H, use_multimer=True).to(torch.bfloat16).eval()
+    ref_layer = M.TransformerLayer_MINT(E, 2 * E, H, use_multimer=True).double().eval()
+    ref_layer.load_state_dict(layer.state_dict())
+    rng = np.random.default_rng(6)
+    x = torch.from_numpy(rng.standard_normal((T, B, E)).astype(np.float32)).to(torch.bfloat16)
+    cid = torch.from_numpy(two_chain_ids(rng, B, T))
+    kp = torch.zeros(B, T, dtype=torch.bool)
+    kp[1, -5:] = True
+    with torch.no_grad():
+        got, _ = layer._multimer_attention_reference_arith(x, None, kp, chain_ids=cid)
+        ref, _ = ref_layer._multimer_attention(x.double(), None, kp, chain_ids=cid)
+    err = (got.double() - ref).abs()
+    assert float(err.max()) <= 2e-2 + 1e-2 * float(ref.abs().max()), float(err.max())
+    kp[0] = True
+    with torch.no_grad():
+        dead, _ = layer._multimer_attention_reference_arith(x, None, kp, chain_ids=cid)
+    assert torch.isnan(dead[:, 0]).all()
+    holder = torch.nn.Module()
+    holder.layers = torch.nn.ModuleList([layer])
+    M.use_eager_multimer(holder, "reference")
+    assert layer._use_eager_multimer == "reference"
+    with pytest.raises(ValueError):
+        M.use_eager_multimer(holder, "fp16")
+
+
 def test_hip_paths_have_no_cpu_fallback():
     """The fused and combine paths run only in the HIP kernels: CPU tensors
     are refused."""

@@ -206,3 +206,37 @@ def test_mint_650m_width_bf16_two_layers():
     sd = {k: v for k, v in model.state_dict().items()}
     _, emb_ref = mo.mint_forward(sd, tok, cid, 2, 20, norm_eps=torch.finfo(torch.bfloat16).eps)
     _check(res["representations"][2], emb_ref, torch.bfloat16, "650M-width", valid=tok != 1)
+
+
+def test_650m_layers_bf16_long_rows():
+    """Three bf16 TransformerLayer_MINT layers of the 650M width (E=1280,
+    H=20, D=64, FFN 5120) at the benchmark's row length: B=2 two-chain
+    complexes of 1006 and 951 tokens (chains >= 64), fused path. Each layer
+    is checked on its own input (the previous GPU layer's output) against
+    the layer oracle in float64 on the same bf16 weights, so bf16 errors of
+    earlier layers do not compound: per element 2e-2 + 1e-2 |ref| at valid
+    rows, and relative Frobenius error <= 1e-2."""
+    print("[650M-width layers, L=1006]", flush=True)
+    M, _, _ = _mods()
+    torch.manual_seed(66)
+    T, B, E, H = 1006, 2, 1280, 20
+    rng = np.random.default_rng(1006)
+    cid = torch.ones(B, T, dtype=torch.int32)
+    kp = torch.zeros(B, T, dtype=torch.bool)
+    for b, n in enumerate((1006, 951)):
+        cid[b, :int(rng.integers(64, n - 64 + 1))] = 0
+        kp[b, n:] = True
+    x = torch.from_numpy(rng.standard_normal((T, B, E)).astype(np.float32)).to(torch.bfloat16)
+    valid = ~kp.transpose(0, 1)  # (T, B)
+    for i in range(3):
+        layer = M.TransformerLayer_MINT(E, 4 * E, H, use_multimer=True).to(DEV, torch.bfloat16).eval()
+        layer._use_fused_multi_pathway = True
+        with torch.no_grad():
+            y, _ = layer(x.to(DEV), self_attn_padding_mask=kp.to(DEV), chain_ids=cid.to(DEV))
+        torch.cuda.synchronize()
+        ref = _oracle_layer(layer, x, cid, kp, H)
+        _check(y, ref, torch.bfloat16, f"650M-width layer {i} L=1006", valid=valid)
+        g, r = y.double().cpu()[valid], ref[valid]
+        rel = float((g - r).norm() / r.norm())
+        assert rel <= 1e-2, (i, rel)
+        x = y.cpu()
