@@ -28,12 +28,17 @@
 //                  softmax rescale is a per-lane multiply. The running max is
 //                  lazy: it moves only when a chunk exceeds it by 2^8.
 //                  STATS mode writes (lse, Delta = dO . O) instead of O.
+//                  16-bit inputs with 16-byte rows take combine_fwd_dma_kernel
+//                  instead: the same math on logit / mask / V tiles copied
+//                  into an LDS ring with row-contiguous global_load_lds.
 //   combine_bwd:   key-stationary; P tiles are recomputed from coalesced
 //                  logit loads and transposed through LDS, dV^T = dO^T P and
 //                  dW^T = V dO^T on MFMA, then dS = P (dW - Delta) goes out as
 //                  both d_logits with coalesced stores.
 // fp32 uses the 32x32x2 fp32 MFMA with the same lane-to-query mapping.
 #include <math.h>
+
+#include <type_traits>
 
 #include "mpattn_common.h"
 
@@ -373,6 +378,274 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(CombineArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Forward (and statistics pass) for 16-bit logits with 16-byte rows: the
+// logit and mask tiles are copied into LDS with global_load_lds, four lanes
+// per 64-byte row segment (row-contiguous reads instead of one 16-byte piece
+// of 32 different rows per instruction), in a ring of NB stages of 32 keys
+// per wavefront, so each wavefront keeps NB-1 stages of its logits in flight
+// without holding them in registers. The V tiles of both pathways (32 keys,
+// shared by the workgroup) ride in the same ring, stored row-major with the
+// fused kernels' chunk swizzle and read transposed (ds_read_b64_tr_b16) as
+// the A operand. Each lane then reads its 8 keys of its own query row from
+// LDS (16-byte chunks XOR-swizzled by row: conflict-free) and runs the same
+// lazy-max online softmax and MFMA accumulation as combine_fwd_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kCKC = 32;  // keys per stage
+#ifndef MPATTN_COMB_NB
+#define MPATTN_COMB_NB 2
+#endif
+constexpr int kCNB = MPATTN_COMB_NB;  // stages in the ring
+
+template <int D> struct CombTile {
+    using TS = TileShape<D>;
+    static constexpr int VT = kCKC * TS::RB;          // bytes of one V tile (32 rows)
+    static constexpr int VSLOTS = kCKC * TS::NCH;     // 16-byte chunks per V tile
+    static constexpr int VINS = (VSLOTS + 63) / 64;   // copy instructions per V tile
+    static constexpr int LG = 32 * kCKC * 2;          // one logit tile: 32 rows x 32 keys (16-bit)
+    static constexpr int MK = 32 * kCKC;              // mask tile: 32 rows x 32 bytes
+    static constexpr int WAVE = 2 * LG + MK;          // per-wave part of a stage
+    static constexpr int STAGE = 4 * WAVE + 2 * VT;   // one ring stage of the workgroup
+};
+
+template <typename T, int D, bool STATS, bool DROPK>
+__global__ __launch_bounds__(256) void combine_fwd_dma_kernel(CombineArgs a) {
+    using TS = TileShape<D>;
+    using CT_ = CombTile<D>;
+    constexpr int ND = (D + 31) / 32;
+    typedef typename Elt<T>::v8 v8;
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(1024))) char smem[kCNB * CT_::STAGE];
+
+    const int L = a.L;
+    const int nqb = (L + 127) / 128;
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = bid / nqb, qb = bid - bh * nqb;
+    int b, h;
+    decode_bh(bh, a.H, b, h);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 31, half = lane >> 5;
+    const int q = qb * 128 + wave * 32 + col;
+    const int qc = min(q, L - 1);
+    // copy bases: the wave's first (clamped) row; rows past L re-read row L-1
+    const int q0c = min(qb * 128 + wave * 32, L - 1);
+    const char* il_b = (const char*)((const T*)a.il + b * a.il_sb + h * a.il_sh + (int64_t)q0c * a.il_st);
+    const char* el_b = (const char*)((const T*)a.el + b * a.el_sb + h * a.el_sh + (int64_t)q0c * a.el_st);
+    const char* m_b = (const char*)(a.mask + b * a.m_sb + (int64_t)q0c * a.m_sq);
+    const char* vs_b = (const char*)((const T*)a.vs + b * a.vs_sb + h * a.vs_sh);
+    const char* vm_b = (const char*)((const T*)a.vm + b * a.vm_sb + h * a.vm_sh);
+    const unsigned il_rs = (unsigned)(a.il_st * 2), el_rs = (unsigned)(a.el_st * 2);
+    const unsigned m_rs = (unsigned)a.m_sq;
+    const unsigned vs_rs = (unsigned)(a.vs_st * 2), vm_rs = (unsigned)(a.vm_st * 2);
+
+    // Per-lane copy offsets. Logits: instruction j covers rows 16j + lane/4,
+    // physical 16-byte chunk lane%4 holding logical chunk (lane%4) ^ swizzle.
+    int lrow[2], lchk[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int r = 16 * j + (lane >> 2);
+        lrow[j] = min(q0c + r, L - 1) - q0c;
+        lchk[j] = (lane & 3) ^ ((r >> 2) & 3);
+    }
+    const int mrow = min(q0c + (lane >> 1), L - 1) - q0c, mchk = lane & 1;
+    const unsigned smem_base = lds_addr(smem);
+
+    // Copy stage t (keys kc = 32 t ..) into ring slot bf; returns the number
+    // of copy instructions this wave issued.
+    auto issue = [&](int t, int bf) -> int {
+        const int kc = t * kCKC;
+        const unsigned sb = __builtin_amdgcn_readfirstlane(smem_base + bf * CT_::STAGE);
+        const unsigned wb = sb + wave * CT_::WAVE;
+        const int m0v = m0_save();
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            // a chunk starting at or past L is read from the row start (its keys are masked)
+            const int k0 = kc + 8 * lchk[j];
+            const unsigned cb = k0 < L ? (unsigned)k0 * 2u : 0u;
+            dma16(il_b, (unsigned)lrow[j] * il_rs + cb, wb + j * 1024);
+            dma16(el_b, (unsigned)lrow[j] * el_rs + cb, wb + CT_::LG + j * 1024);
+        }
+        {
+            const int k0 = kc + 16 * mchk;
+            dma16(m_b, (unsigned)mrow * m_rs + (k0 < L ? (unsigned)k0 : 0u), wb + 2 * CT_::LG);
+        }
+        int n = 5;
+        // V tiles: instruction i of 2*VINS, spread over the waves
+#pragma unroll
+        for (int i = wave; i < 2 * CT_::VINS; i += 4) {
+            const int ten = i / CT_::VINS, part = i % CT_::VINS;
+            const int slot = part * 64 + lane;
+            const unsigned ld = __builtin_amdgcn_readfirstlane(sb + 4 * CT_::WAVE + ten * CT_::VT + part * 1024);
+            const int r = min(slot, CT_::VSLOTS - 1) / TS::NCH;
+            const int cbv = TS::swz(r, slot % TS::NCH) * 16;
+            const unsigned vo = (unsigned)min(kc + r, L - 1) * (ten ? vm_rs : vs_rs) + cbv;
+            if constexpr (CT_::VSLOTS % 64 == 0) {
+                dma16(ten ? vm_b : vs_b, vo, ld);
+            } else if (slot < CT_::VSLOTS) {  // (D = 24: the last copy has 32 lanes)
+                dma16(ten ? vm_b : vs_b, vo, ld);
+            }
+            ++n;
+        }
+        m0_restore(m0v);
+        return n;
+    };
+
+    // V^T operand (as the fused forward): lane (tg, ti) reads rows
+    // 8*(tg>>1) + 4*rr + ti/4 of chunk 8*db + 4*(tg&1) + ti%4 (8-byte halves).
+    const int tg = lane >> 4, ti = lane & 15;
+    int voffv[ND][2];
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+        int e = 8 * db + 4 * (tg & 1) + (ti & 3);
+        if (8 * e >= TS::RB) e = ti & 3;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int row = 8 * (tg >> 1) + 4 * rr + (ti >> 2);
+            voffv[db][rr] = row * TS::RB + TS::swz(row, e >> 1) * 16 + (e & 1) * 8;
+        }
+    }
+    auto vop = [&](const char* tile, int cc, int db) -> v8 {
+        s4 hv[2];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr)
+            hv[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s4*)(tile + 16 * cc * TS::RB + voffv[db][rr]));
+        return __builtin_bit_cast(v8, __builtin_shufflevector(hv[0], hv[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+
+    f32x16 acc[ND];
+#pragma unroll
+    for (int n = 0; n < ND; ++n)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[n][i] = 0.f;
+    float mref = -INFINITY, lsum = 0.f;
+    const bool dropon = DROPK && a.drop_on != 0;
+    const uint32_t drow = dropon ? drop_row(a.drop.lo, (uint32_t)bh, (uint32_t)q) : 0u;
+
+    const int nst = (L + kCKC - 1) / kCKC;
+    int pend[kCNB];
+#pragma unroll
+    for (int t = 0; t < kCNB; ++t) pend[t] = 0;
+#pragma unroll
+    for (int t = 0; t < kCNB - 1; ++t)
+        if (t < nst) pend[t] = issue(t, t);
+    int bf = 0;
+    for (int t = 0; t < nst; ++t) {
+        int allow = 0;
+#pragma unroll
+        for (int k = 1; k < kCNB - 1; ++k) allow += pend[k];
+        wait_vm_var(allow);
+        stage_barrier();
+#pragma unroll
+        for (int k = 0; k < kCNB - 1; ++k) pend[k] = pend[k + 1];
+        pend[kCNB - 1] = 0;
+        if (t + kCNB - 1 < nst) pend[kCNB - 2] = issue(t + kCNB - 1, bf == 0 ? kCNB - 1 : bf - 1);
+        const char* sg = smem + bf * CT_::STAGE;
+        const char* wb = sg + wave * CT_::WAVE;
+        const char* vst = sg + 4 * CT_::WAVE;
+        const int kc = t * kCKC;
+        // TAIL: the last stage, whose keys past L are masked
+        auto stage_steps = [&](auto tail_c) {
+            constexpr bool tail = decltype(tail_c)::value;
+#pragma unroll
+        for (int ks = 0; ks < kCKC / 16; ++ks) {
+            const int k = kc + ks * 16 + half * 8;
+            const int lc = ks * 2 + half;  // logical 16-byte chunk of the row
+            const int pc = lc ^ ((col >> 2) & 3);
+            const v8 ri = *reinterpret_cast<const v8*>(wb + col * 64 + pc * 16);
+            const v8 re = *reinterpret_cast<const v8*>(wb + CT_::LG + col * 64 + pc * 16);
+            const uint2 mw = *reinterpret_cast<const uint2*>(wb + 2 * CT_::LG + col * 32 + ks * 16 + half * 8);
+            // Selected raw logits (natural units; the log2(e) factor goes into
+            // the exp2 argument) and their max.
+            bool x[8];
+            float v[8];
+            float cm = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                x[j] = (((j < 4 ? mw.x : mw.y) >> (8 * (j & 3))) & 0xffu) != 0;
+                v[j] = x[j] ? (float)re[j] : (float)ri[j];
+                if (tail && k + j >= L) v[j] = -INFINITY;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) cm = fmaxf(cm, fmaxf(v[j], v[j + 1]));
+            cm = fmaxf(cm, __shfl_xor(cm, 32)) * kLog2eC;
+            if (__any(cm > mref + kLazy)) {
+                const float mn = fmaxf(mref, cm);
+                const float f = (mn == -INFINITY) ? 1.f : fast_exp2(mref - mn);
+#pragma unroll
+                for (int n = 0; n < ND; ++n)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) acc[n][i] *= f;
+                lsum *= f;
+                mref = mn;
+            }
+            const float mu = (mref == -INFINITY) ? 0.f : mref;
+            float pi[8], pe[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float p = fast_exp2(fmaf(v[j], kLog2eC, -mu));
+                lsum += p;  // the row sum is over the undropped P
+                if (dropon && !drop_keep(drow, a.drop.hi, (uint32_t)(k + j), a.drop.thr)) p = 0.f;
+                pi[j] = x[j] ? 0.f : p;
+                pe[j] = x[j] ? p : 0.f;
+            }
+            const v8 bi = pack8<T>(pi), be = pack8<T>(pe);
+#pragma unroll
+            for (int n = 0; n < ND; ++n) {
+                acc[n] = Elt<T>::mma(vop(vst, ks, n), bi, acc[n]);
+                acc[n] = Elt<T>::mma(vop(vst + CT_::VT, ks, n), be, acc[n]);
+            }
+        }
+        };
+        if (kc + kCKC > L) stage_steps(std::true_type{});
+        else stage_steps(std::false_type{});
+        bf = bf + 1 == kCNB ? 0 : bf + 1;
+    }
+
+    const float lt = lsum + __shfl_xor(lsum, 32);
+    const float inv = lt > 0.f ? (dropon ? a.drop.rkeep : 1.f) / lt : 0.f;
+    const int64_t row = (int64_t)bh * L + qc;
+    if (a.lse && q < L && half == 0) {
+        const float mu = (mref == -INFINITY) ? 0.f : mref;
+        a.lse[row] = lt > 0.f ? (mu + __log2f(lt)) * kLn2 : -INFINITY;
+    }
+    if constexpr (STATS) {
+        const T* g = (const T*)a.go + b * a.g_sb + h * a.g_sh + (int64_t)qc * a.g_st;
+        float dot = 0.f;
+#pragma unroll
+        for (int n = 0; n < ND; ++n)
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const int d = n * 32 + gi * 8 + half * 4;
+                if (d < D) {
+                    float gg[4];
+                    load4f<T>(g, d, gg);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) dot += gg[r] * acc[n][gi * 4 + r];
+                }
+            }
+        dot = (dot + __shfl_xor(dot, 32)) * inv;
+        if (q < L && half == 0) a.delta[row] = dot;
+    } else {
+        if (q < L) {
+            T* o = (T*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)q * a.o_st;
+#pragma unroll
+            for (int n = 0; n < ND; ++n)
+#pragma unroll
+                for (int gi = 0; gi < 4; ++gi) {
+                    const int d = n * 32 + gi * 8 + half * 4;
+                    if (d < D) {
+                        float v[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) v[r] = acc[n][gi * 4 + r] * inv;
+                        store4<T>(o, d, v);
+                    }
+                }
+        }
+    }
+}
+
 // 8 consecutive elements of a row from fp32 values (k % 8 == 0, row 16-byte
 // aligned).
 template <typename T>
@@ -657,10 +930,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ND == 1 ? 4
     }
 }
 
+bool aligned_rows(const void* p, int64_t sb, int64_t sh, int64_t st, int es);
+
+// The DMA-staged forward / statistics pass for 16-bit inputs whose logit,
+// mask and value rows are 16-byte aligned (mask bytes unit-strided).
+bool dma_ok(const CombineArgs& a) {
+    const bool lg = aligned_rows(a.il, a.il_sb, a.il_sh, a.il_st, 2) && aligned_rows(a.el, a.el_sb, a.el_sh, a.el_st, 2);
+    const bool mk = a.m_sk == 1 && (uintptr_t)a.mask % 16 == 0 && a.m_sb % 16 == 0 && a.m_sq % 16 == 0;
+    const bool v = aligned_rows(a.vs, a.vs_sb, a.vs_sh, a.vs_st, 2) && aligned_rows(a.vm, a.vm_sb, a.vm_sh, a.vm_st, 2);
+    return lg && mk && v;
+}
+
+template <typename T, int D, bool STATS>
+void launch_dma_d(const CombineArgs& a, hipStream_t st) {
+    const unsigned grid = (unsigned)(a.B * a.H * ((a.L + 127) / 128));
+    if (a.drop_on)
+        hipLaunchKernelGGL((combine_fwd_dma_kernel<T, D, STATS, true>), dim3(grid), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((combine_fwd_dma_kernel<T, D, STATS, false>), dim3(grid), dim3(256), 0, st, a);
+}
+
+template <typename T, bool STATS>
+void launch_dma(const CombineArgs& a, hipStream_t st) {
+    switch (a.D) {
+        case 16: launch_dma_d<T, 16, STATS>(a, st); break;
+        case 24: launch_dma_d<T, 24, STATS>(a, st); break;
+        case 32: launch_dma_d<T, 32, STATS>(a, st); break;
+        default: launch_dma_d<T, 64, STATS>(a, st); break;
+    }
+}
+
 template <typename T, int ND, bool VEC>
 hipError_t launch_combine_t(const CombineArgs& a, int mode, hipStream_t st) {
     const int nqb = (a.L + 127) / 128, nkb = (a.L + 63) / 64;
     const int bh = a.B * a.H;
+    if constexpr (sizeof(T) == 2 && VEC) {
+        if (dma_ok(a)) {
+            if (mode == 0) {
+                launch_dma<T, false>(a, st);
+                return hipGetLastError();
+            }
+            launch_dma<T, true>(a, st);
+            hipLaunchKernelGGL((combine_bwd_kernel<T, ND, VEC>), dim3(bh * nkb), dim3(256), 0, st, a);
+            return hipGetLastError();
+        }
+    }
     // Without dropout the forward is instantiated with no dropout code.
     if (mode == 0) {
         if (a.drop_on)

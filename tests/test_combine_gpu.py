@@ -55,8 +55,11 @@ def check(got, ref, dtype, what, rel_fro=None):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("D", [16, 24, 32, 64])
-@pytest.mark.parametrize("L", [64, 100, 257])
+@pytest.mark.parametrize("L", [16, 64, 100, 208, 257])
 def test_combine_fwd(dtype, D, L):
+    """L = 16, 64, 208 (16-bit rows of 16-byte multiples): the copy-staged
+    kernel, with a partial last key stage (16, 208) and query blocks past L;
+    L = 100, 257: the register-load kernel."""
     print(f"[combine fwd] {dtype} D={D} L={L}", flush=True)
     t, cm = make(2, 3, L, D, dtype, seed=100 + D + L)
     out = _m().fused_multimer_combine(*[x.to(DEV) for x in t[:2]], torch.from_numpy(cm).to(DEV),
@@ -69,7 +72,7 @@ def test_combine_fwd(dtype, D, L):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("D", [16, 32, 64])
-@pytest.mark.parametrize("L", [64, 129])
+@pytest.mark.parametrize("L", [64, 129, 208])
 def test_combine_bwd(dtype, D, L):
     print(f"[combine bwd] {dtype} D={D} L={L}", flush=True)
     t, cm = make(2, 2, L, D, dtype, seed=200 + D + L)
