@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define MPATTN_VERSION 4
+#define MPATTN_VERSION 5
 
 enum {
     MPATTN_OK = 0,
@@ -95,8 +95,8 @@ typedef struct mpattn_fwd_params {
     int32_t rope;            /* MPATTN_ROPE_NONE / MPATTN_ROPE_FUSED         */
     float scale;             /* logit scale (> 0), e.g. D^-1/2               */
     int32_t sqrt_softmax;    /* 1: O = sum sqrt(P) V (muS variant)           */
-    float dropout_p;         /* attention dropout in [0, 1); > 0 needs 16-bit
-                                inputs and sqrt_softmax == 0               */
+    float dropout_p;         /* attention dropout in [0, 1) (with sqrt_softmax
+                                it drops the sqrt(P) weights)              */
     void *workspace;         /* >= mpattn_fwd_workspace_size() bytes, 256-byte
                                 aligned; contents need no initialisation   */
     int64_t workspace_bytes;
@@ -125,8 +125,9 @@ typedef struct mpattn_bwd_params {
     uint64_t dropout_seed;
 } mpattn_bwd_params;
 
-/* Attention dropout. Element (b, h, i, j) of P is kept, and scaled by
- * 1 / (1 - dropout_p), when
+/* Attention dropout. Element (b, h, i, j) of the weights that multiply V
+ * (P, or sqrt(P) with sqrt_softmax) is kept, and scaled by 1 / (1 - dropout_p),
+ * when
  *   r = fmix32(fmix32(lo ^ (b*H + h) * 0xC2B2AE3D ^ i * 0x9E3779B1)
  *              ^ (j * 0x85EBCA77 + hi))
  * has (r >> 8) >= round(dropout_p * 2^24), with lo / hi the low / high 32 bits

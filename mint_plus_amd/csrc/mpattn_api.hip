@@ -87,13 +87,12 @@ int check_common(int B, int H, int L, int D, int dtype, int rope, float scale,
     return MPATTN_OK;
 }
 
-// Attention dropout: p in [0, 1); p > 0 is built for the 16-bit softmax
-// kernels only.
+// Attention dropout: p in [0, 1) (every element type, with or without
+// sqrt-softmax).
 int check_dropout(float p, int dtype, int sqrt_softmax) {
+    (void)dtype;
+    (void)sqrt_softmax;
     if (!(p >= 0.f && p < 1.f)) return fail(MPATTN_ERR_INVALID, "dropout_p must be in [0, 1) (got %g)", (double)p);
-    if (p > 0.f && dtype == MPATTN_FP32)
-        return fail(MPATTN_ERR_UNSUPPORTED, "dropout_p > 0 needs bf16 or fp16 inputs");
-    if (p > 0.f && sqrt_softmax) return fail(MPATTN_ERR_UNSUPPORTED, "dropout_p > 0 with sqrt_softmax is not built");
     return MPATTN_OK;
 }
 

@@ -1085,11 +1085,17 @@ template <typename T, int D>
 static hipError_t dispatch_bwd_d(const mpattn_bwd_params& p, hipStream_t s) {
     const bool rope = p.rope == MPATTN_ROPE_FUSED;
     const bool dense = p.chain_mask != nullptr;
-    if (p.sqrt_softmax) {  // (dropout with sqrt-softmax is rejected by the API)
+    // fp32: dropout is handled by the fp32 kernels' own dispatch.
+    const bool drop = p.dropout_p > 0.f && !std::is_same<T, float>::value;
+    if (p.sqrt_softmax) {
+        if (drop) {
+            if (rope) return dense ? launch_bwd_t<T, D, true, true, true, true>(p, s) : launch_bwd_t<T, D, true, false, true, true>(p, s);
+            return dense ? launch_bwd_t<T, D, false, true, true, true>(p, s) : launch_bwd_t<T, D, false, false, true, true>(p, s);
+        }
         if (rope) return dense ? launch_bwd_t<T, D, true, true, true, false>(p, s) : launch_bwd_t<T, D, true, false, true, false>(p, s);
         return dense ? launch_bwd_t<T, D, false, true, true, false>(p, s) : launch_bwd_t<T, D, false, false, true, false>(p, s);
     }
-    if (p.dropout_p > 0.f && !std::is_same<T, float>::value) {  // (no fp32 dropout: rejected by the API)
+    if (drop) {
         if (rope) return dense ? launch_bwd_t<T, D, true, true, false, true>(p, s) : launch_bwd_t<T, D, true, false, false, true>(p, s);
         return dense ? launch_bwd_t<T, D, false, true, false, true>(p, s) : launch_bwd_t<T, D, false, false, false, true>(p, s);
     }

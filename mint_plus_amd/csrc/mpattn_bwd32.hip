@@ -13,6 +13,8 @@
 //                  dV_j += w_ij dO_i,  dS_ij = w_ij (dP_ij - w_ij Delta_i) / 2
 //   dP_ij = dO_i . V_sel,j;  dQ_i = scale sum_j dS_ij K_sel,j;
 //   dK_j = kmul sum_i dS_ij Q_sel,i;  R^T applied to dQ_self and dK_self.
+//   With dropout (keep mask Z, r = 1 / (1 - p)): dV takes r Z w and dP_ij
+//   becomes r Z_ij dO_i . V_sel,j (the forward's definition in mpattn.h).
 //
 // Both kernels split the work by pathway: a workgroup computes the gradients
 // of one pathway only, so it needs one pathway's operands and accumulators
@@ -151,7 +153,7 @@ struct Shape32 {
 // ---------------------------------------------------------------------------
 // dK / dV of pathway PW for 128 keys.
 // ---------------------------------------------------------------------------
-template <int D, bool ROPE, bool DENSE, bool SQRT, int PW>
+template <int D, bool ROPE, bool DENSE, bool SQRT, bool DROP, int PW>
 __device__ void dkdv32_body(const BwdArgs& a, float* smem, int* sint, int kb, int b, int h) {
     using S = Shape32<D>;
     constexpr int NK = S::NK, NDB = S::NDB, RS = S::RS, TILE = S::TILE;
@@ -258,14 +260,16 @@ __device__ void dkdv32_body(const BwdArgs& a, float* smem, int* sint, int kb, in
                 const float l2 = __int_as_float(si[ql]);
                 const float dl = __int_as_float(si[kTB + ql]);
                 const float pr = on ? fast_exp2(s[i] * c - l2) : 0.f;
-                if constexpr (SQRT) {
-                    const float w = sqrtf(pr);
-                    wv[i] = w;
-                    ds[i] = 0.5f * w * (dp[i] - w * dl);
-                } else {
-                    wv[i] = pr;
-                    ds[i] = pr * (dp[i] - dl);
+                const float w = SQRT ? sqrtf(pr) : pr;
+                float dpi = dp[i];
+                bool keep = true;
+                if constexpr (DROP) {
+                    keep = drop_keep(drop_row(a.drop.lo, (uint32_t)(b * p.H + h), (uint32_t)(t * kTB + ql)),
+                                     a.drop.hi, (uint32_t)key, a.drop.thr);
+                    dpi = keep ? dpi * a.drop.rkeep : 0.f;
                 }
+                wv[i] = keep ? w : 0.f;  // (1 / (1 - p) applied when dV is stored)
+                ds[i] = SQRT ? 0.5f * w * (dpi - w * dl) : w * (dpi - dl);
             }
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
@@ -286,13 +290,14 @@ __device__ void dkdv32_body(const BwdArgs& a, float* smem, int* sint, int kb, in
     const mpattn_tensor& dvt = PW == 0 ? p.dv_self : p.dv_multi;
     const mpattn_tensor& dkt = PW == 0 ? p.dk_self : p.dk_multi;
     if (kw0 < L) {
-        store_rows32<D>(dv, scratch, dvt, b, h, kw0, L, 1.0f, false, nullptr, nullptr, key_live);
+        store_rows32<D>(dv, scratch, dvt, b, h, kw0, L, DROP ? a.drop.rkeep : 1.0f, false, nullptr, nullptr,
+                        key_live);
         store_rows32<D>(dk, scratch, dkt, b, h, kw0, L, a.kmul, ROPE && PW == 0, p.rope_cos, p.rope_sin,
                         key_live);
     }
 }
 
-template <int D, bool ROPE, bool DENSE, bool SQRT>
+template <int D, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 __global__ __launch_bounds__(256) void bwd32_dkdv_kernel(const BwdArgs a) {
     __shared__ float smem[Shape32<D>::SMEM];
     __shared__ int sint[2 * 3 * kTB];
@@ -301,14 +306,14 @@ __global__ __launch_bounds__(256) void bwd32_dkdv_kernel(const BwdArgs a) {
     const int pw = g & 1, rest = g >> 1;
     const int kb = rest % nkb, bh = rest / nkb;
     const int b = bh / a.p.H, h = bh % a.p.H;
-    if (pw == 0) dkdv32_body<D, ROPE, DENSE, SQRT, 0>(a, smem, sint, kb, b, h);
-    else dkdv32_body<D, ROPE, DENSE, SQRT, 1>(a, smem, sint, kb, b, h);
+    if (pw == 0) dkdv32_body<D, ROPE, DENSE, SQRT, DROP, 0>(a, smem, sint, kb, b, h);
+    else dkdv32_body<D, ROPE, DENSE, SQRT, DROP, 1>(a, smem, sint, kb, b, h);
 }
 
 // ---------------------------------------------------------------------------
 // dQ of pathway PW for 128 queries.
 // ---------------------------------------------------------------------------
-template <int D, bool ROPE, bool DENSE, bool SQRT, int PW>
+template <int D, bool ROPE, bool DENSE, bool SQRT, bool DROP, int PW>
 __device__ void dq32_body(const BwdArgs& a, float* smem, int* sint, int qb, int b, int h) {
     using S = Shape32<D>;
     constexpr int NK = S::NK, NDB = S::NDB, RS = S::RS, TILE = S::TILE;
@@ -333,6 +338,7 @@ __device__ void dq32_body(const BwdArgs& a, float* smem, int* sint, int qb, int 
     const int64_t rowi = ((int64_t)b * H + h) * Lp + (qvalid ? q : 0);
     const float l2 = qvalid ? a.lse2[rowi] : INFINITY;
     const float dl = qvalid ? a.delta[rowi] : 0.f;
+    const uint32_t drow = DROP ? drop_row(a.drop.lo, (uint32_t)(b * H + h), (uint32_t)q) : 0u;
     const int cq = qvalid ? a.qcid[(int64_t)b * Lp + q] : 0;
     int qmin = 0, qmax = -1;
     if (qw0 < L) {
@@ -404,12 +410,11 @@ __device__ void dq32_body(const BwdArgs& a, float* smem, int* sint, int qb, int 
                     on = ck != kPadChain && (same == (PW == 0));
                 }
                 const float pr = on ? fast_exp2(s[i] * c - l2) : 0.f;
-                if constexpr (SQRT) {
-                    const float w = sqrtf(pr);
-                    ds[i] = 0.5f * w * (dp[i] - w * dl);
-                } else {
-                    ds[i] = pr * (dp[i] - dl);
-                }
+                const float w = SQRT ? sqrtf(pr) : pr;
+                float dpi = dp[i];
+                if constexpr (DROP)
+                    dpi = drop_keep(drow, a.drop.hi, (uint32_t)(t * kTB + kl), a.drop.thr) ? dpi * a.drop.rkeep : 0.f;
+                ds[i] = SQRT ? 0.5f * w * (dpi - w * dl) : w * (dpi - dl);
             }
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
@@ -430,7 +435,7 @@ __device__ void dq32_body(const BwdArgs& a, float* smem, int* sint, int qb, int 
                         ROPE && PW == 0, p.rope_cos, p.rope_sin, 0xffffffffu);
 }
 
-template <int D, bool ROPE, bool DENSE, bool SQRT>
+template <int D, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 __global__ __launch_bounds__(256) void bwd32_dq_kernel(const BwdArgs a) {
     __shared__ float smem[Shape32<D>::SMEM];
     __shared__ int sint[2 * kTB];
@@ -439,26 +444,26 @@ __global__ __launch_bounds__(256) void bwd32_dq_kernel(const BwdArgs a) {
     const int pw = g & 1, rest = g >> 1;
     const int qb = rest % nqb, bh = rest / nqb;
     const int b = bh / a.p.H, h = bh % a.p.H;
-    if (pw == 0) dq32_body<D, ROPE, DENSE, SQRT, 0>(a, smem, sint, qb, b, h);
-    else dq32_body<D, ROPE, DENSE, SQRT, 1>(a, smem, sint, qb, b, h);
+    if (pw == 0) dq32_body<D, ROPE, DENSE, SQRT, DROP, 0>(a, smem, sint, qb, b, h);
+    else dq32_body<D, ROPE, DENSE, SQRT, DROP, 1>(a, smem, sint, qb, b, h);
 }
 
-template <int D, bool ROPE, bool DENSE, bool SQRT>
+template <int D, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 hipError_t launch32(const BwdArgs& a, hipStream_t stream) {
     const int nb = (a.p.L + 127) / 128;
     const unsigned grid = (unsigned)(2 * (int64_t)a.p.B * a.p.H * nb);
-    hipLaunchKernelGGL((bwd32_dkdv_kernel<D, ROPE, DENSE, SQRT>), dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((bwd32_dkdv_kernel<D, ROPE, DENSE, SQRT, DROP>), dim3(grid), dim3(256), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd32_dq_kernel<D, ROPE, DENSE, SQRT>), dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((bwd32_dq_kernel<D, ROPE, DENSE, SQRT, DROP>), dim3(grid), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
-template <int D>
-hipError_t dispatch32(const BwdArgs& a, hipStream_t s) {
+template <int D, bool DROP>
+hipError_t dispatch32_d(const BwdArgs& a, hipStream_t s) {
     const bool rope = a.p.rope == MPATTN_ROPE_FUSED, dense = a.p.chain_mask != nullptr;
     const bool sq = a.p.sqrt_softmax != 0;
-#define MPATTN_B32(R, DN, SQ) return launch32<D, R, DN, SQ>(a, s)
+#define MPATTN_B32(R, DN, SQ) return launch32<D, R, DN, SQ, DROP>(a, s)
     if (rope) {
         if (dense) { if (sq) MPATTN_B32(true, true, true); MPATTN_B32(true, true, false); }
         if (sq) MPATTN_B32(true, false, true);
@@ -468,6 +473,12 @@ hipError_t dispatch32(const BwdArgs& a, hipStream_t s) {
     if (sq) MPATTN_B32(false, false, true);
     MPATTN_B32(false, false, false);
 #undef MPATTN_B32
+}
+
+template <int D>
+hipError_t dispatch32(const BwdArgs& a, hipStream_t s) {
+    if (a.p.dropout_p > 0.f) return dispatch32_d<D, true>(a, s);
+    return dispatch32_d<D, false>(a, s);
 }
 
 }  // namespace

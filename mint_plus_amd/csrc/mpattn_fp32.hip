@@ -36,10 +36,13 @@ __device__ __forceinline__ f32x16 mma32(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-template <int D, bool ROPE, bool DENSE, bool SQRT>
+// DROP: attention dropout (the definition in mpattn.h): the weights that
+// multiply V are the kept ones, the row sum takes all of them, and O is
+// scaled by 1 / (1 - p).
+template <int D, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 __global__ __launch_bounds__(256) void fwd32_kernel(const mpattn_fwd_params p, const int* keff,
                                                     const int* ksum, const int* qsum, int Lp,
-                                                    float qmul, float c) {
+                                                    float qmul, float c, DropCfg drop) {
     constexpr int W = 4;
     constexpr int H2 = D / 2;
     constexpr int NK = D / 2;             // MFMA steps over head dims
@@ -62,6 +65,7 @@ __global__ __launch_bounds__(256) void fwd32_kernel(const mpattn_fwd_params p, c
     const int qw0 = qb * 32 * W;
     const int q = qw0 + wave * 32 + ql;
     const bool qvalid = q < L;
+    const uint32_t drow = DROP ? drop_row(drop.lo, (uint32_t)bh, (uint32_t)q) : 0u;
 
     auto base = [&](const mpattn_tensor& t) {
         return (const float*)t.ptr + b * t.stride_b + h * t.stride_h;
@@ -235,6 +239,8 @@ __global__ __launch_bounds__(256) void fwd32_kernel(const mpattn_fwd_params p, c
                 const float pr = fast_exp2(s[i] - mr);  // 0 for padded keys
                 l_run += pr;
                 w[i] = SQRT ? sqrtf(pr) : pr;
+                if constexpr (DROP)
+                    if (!drop_keep(drow, drop.hi, (uint32_t)(t * kKB + 2 * i + hh), drop.thr)) w[i] = 0.f;
                 const bool sm_ = (same >> i) & 1u;
                 ws[i] = sm_ ? w[i] : 0.f;
                 wm[i] = sm_ ? 0.f : w[i];
@@ -250,7 +256,7 @@ __global__ __launch_bounds__(256) void fwd32_kernel(const mpattn_fwd_params p, c
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32);
-    const float inv = l_tot > 0.f ? (SQRT ? 1.0f / sqrtf(l_tot) : 1.0f / l_tot) : 0.f;
+    const float inv = l_tot > 0.f ? (SQRT ? 1.0f / sqrtf(l_tot) : 1.0f / l_tot) * (DROP ? drop.rkeep : 1.0f) : 0.f;
     if (qvalid) {
         float* orow = (float*)p.out.ptr + b * p.out.stride_b + h * p.out.stride_h + (int64_t)q * p.out.stride_t;
 #pragma unroll
@@ -272,7 +278,7 @@ __global__ __launch_bounds__(256) void fwd32_kernel(const mpattn_fwd_params p, c
     }
 }
 
-template <int D, bool ROPE, bool DENSE, bool SQRT>
+template <int D, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 hipError_t launch32(const mpattn_fwd_params& p, const int* keff, const int* ksum, const int* qsum, int Lp,
                     hipStream_t stream) {
     const float f = p.scale * kLog2e;
@@ -280,16 +286,17 @@ hipError_t launch32(const mpattn_fwd_params& p, const int* keff, const int* ksum
     // once either way in fp32); otherwise the factor is applied to the logits.
     const bool fused = ROPE;
     const int nqb = (p.L + 127) / 128;
-    hipLaunchKernelGGL((fwd32_kernel<D, ROPE, DENSE, SQRT>), dim3((unsigned)((int64_t)p.B * p.H * nqb)),
-                       dim3(256), 0, stream, p, keff, ksum, qsum, Lp, fused ? f : 1.0f, fused ? 1.0f : f);
+    hipLaunchKernelGGL((fwd32_kernel<D, ROPE, DENSE, SQRT, DROP>), dim3((unsigned)((int64_t)p.B * p.H * nqb)),
+                       dim3(256), 0, stream, p, keff, ksum, qsum, Lp, fused ? f : 1.0f, fused ? 1.0f : f,
+                       drop_cfg(p.dropout_p, p.dropout_seed));
     return hipGetLastError();
 }
 
-template <int D>
-hipError_t dispatch32(const mpattn_fwd_params& p, const int* keff, const int* ksum, const int* qsum, int Lp,
-                      hipStream_t s) {
+template <int D, bool DROP>
+hipError_t dispatch32_d(const mpattn_fwd_params& p, const int* keff, const int* ksum, const int* qsum, int Lp,
+                        hipStream_t s) {
     const bool rope = p.rope == MPATTN_ROPE_FUSED, dense = p.chain_mask != nullptr, sq = p.sqrt_softmax != 0;
-#define MPATTN_L32(R, DN, SQ) return launch32<D, R, DN, SQ>(p, keff, ksum, qsum, Lp, s)
+#define MPATTN_L32(R, DN, SQ) return launch32<D, R, DN, SQ, DROP>(p, keff, ksum, qsum, Lp, s)
     if (rope) {
         if (dense) { if (sq) MPATTN_L32(true, true, true); MPATTN_L32(true, true, false); }
         if (sq) MPATTN_L32(true, false, true);
@@ -299,6 +306,13 @@ hipError_t dispatch32(const mpattn_fwd_params& p, const int* keff, const int* ks
     if (sq) MPATTN_L32(false, false, true);
     MPATTN_L32(false, false, false);
 #undef MPATTN_L32
+}
+
+template <int D>
+hipError_t dispatch32(const mpattn_fwd_params& p, const int* keff, const int* ksum, const int* qsum, int Lp,
+                      hipStream_t s) {
+    if (p.dropout_p > 0.f) return dispatch32_d<D, true>(p, keff, ksum, qsum, Lp, s);
+    return dispatch32_d<D, false>(p, keff, ksum, qsum, Lp, s);
 }
 
 }  // namespace

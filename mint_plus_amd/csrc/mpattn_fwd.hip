@@ -1193,7 +1193,11 @@ template <typename T, int D>
 static hipError_t dispatch_fwd_d(FwdArgs& a, hipStream_t s) {
     const bool rope = a.p.rope == MPATTN_ROPE_FUSED;
     const bool dense = a.p.chain_mask != nullptr;
-    if (a.p.sqrt_softmax) {  // (dropout with sqrt-softmax is rejected by the API)
+    if (a.p.sqrt_softmax) {
+        if (a.p.dropout_p > 0.f) {
+            if (rope) return dense ? launch_fwd<T, D, true, true, true, true>(a, s) : launch_fwd<T, D, true, false, true, true>(a, s);
+            return dense ? launch_fwd<T, D, false, true, true, true>(a, s) : launch_fwd<T, D, false, false, true, true>(a, s);
+        }
         if (rope) return dense ? launch_fwd<T, D, true, true, true, false>(a, s) : launch_fwd<T, D, true, false, true, false>(a, s);
         return dense ? launch_fwd<T, D, false, true, true, false>(a, s) : launch_fwd<T, D, false, false, true, false>(a, s);
     }

@@ -189,19 +189,11 @@ class TransformerLayer_MINT(nn.Module):
         out = out.transpose(1, 2).reshape(B, T, E)
         return self.self_attn.out_proj(out).transpose(0, 1).contiguous(), None
 
-    def _fused_covers(self, x):
-        """The fused kernels serve 16-bit inputs in every mode and fp32
-        inputs in every mode but training with dropout (fp32 dropout is not
-        built; the combine kernels cover it)."""
-        if x.dtype != torch.float32:
-            return True
-        return not (self.training and self.self_attn.dropout > 0)
-
     def _multimer_attention_plus(self, x, chain_mask, padding_mask, chain_ids=None):
         """Dispatch (modules.py:200-249): fused multi-pathway kernel when the
-        flag is set (and it covers the dtype and mode), else the materialised
-        pipeline with the combine kernel."""
-        if self._use_fused_multi_pathway and self._fused_covers(x):
+        flag is set (every dtype and mode), else the materialised pipeline
+        with the combine kernel."""
+        if self._use_fused_multi_pathway:
             return self._multimer_attention_superfused(x, chain_mask, padding_mask, chain_ids)
         eager = getattr(self, "_use_eager_multimer", False)
         if eager == "reference":

@@ -37,7 +37,7 @@ def test_exports_every_header_function(lib):
 
 
 def test_version_and_strings(lib):
-    assert lib.mpattn_version() == 4
+    assert lib.mpattn_version() == 5
     assert lib.mpattn_strerror(0) == b"success"
     assert lib.mpattn_strerror(-2) == b"unsupported configuration"
     assert lib.mpattn_strerror(-99) == b"unknown error"
@@ -137,8 +137,6 @@ FWD_CASES = [
     (dict(dropout_p=-0.1), _lib.MPATTN_ERR_INVALID, "dropout"),
     (dict(dropout_p=1.0), _lib.MPATTN_ERR_INVALID, "dropout"),
     (dict(dropout_p=float("nan")), _lib.MPATTN_ERR_INVALID, "dropout"),
-    (dict(dropout_p=0.1, dtype=_lib.MPATTN_FP32), _lib.MPATTN_ERR_UNSUPPORTED, "dropout"),
-    (dict(dropout_p=0.1, sqrt_softmax=1), _lib.MPATTN_ERR_UNSUPPORTED, "dropout"),
     (dict(q_self=_lib.Tensor4(None, 0, 0, 32)), _lib.MPATTN_ERR_INVALID, "null"),
     (dict(k_self=_lib.Tensor4((1 << 20) + 8, 40960, 2048, 32)), _lib.MPATTN_ERR_UNSUPPORTED, "aligned"),
     (dict(v_multi=_lib.Tensor4(1 << 20, 40960, 2048, 36)), _lib.MPATTN_ERR_UNSUPPORTED, "multiples"),

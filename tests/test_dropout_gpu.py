@@ -1,4 +1,5 @@
-"""Attention dropout of the fused op (16-bit kernels) against the oracle.
+"""Attention dropout of the fused op (16-bit and fp32 kernels, with and
+without sqrt-softmax) against the oracle.
 
 The keep mask is a function of (seed, b*H + h, query, key) (definition in
 include/mpattn.h, restated by ``oracle.mpattn_oracle.dropout_keep``), so the
@@ -90,12 +91,14 @@ def _step(kp, p):
     return (r / n)[:, None, None, None]
 
 
-EXACT_CASES = [  # (dtype, D, L): L / D groups, at most 4 (bf16) or 8 (fp16)
+EXACT_CASES = [  # (dtype, D, L): L / D groups, at most 4 (bf16), 8 (fp16) or 16 (fp32)
     (torch.bfloat16, 16, 64),
     (torch.bfloat16, 32, 128),
     (torch.bfloat16, 64, 256),
     (torch.float16, 32, 256),
     (torch.float16, 24, 190),
+    (torch.float32, 16, 200),
+    (torch.float32, 32, 256),
 ]
 
 
@@ -144,7 +147,7 @@ def test_dropout_exact_mask_dv(dtype, D, L):
         assert (err <= tol).all(), f"{name}: max err {err.max():.4g} vs {tol.min():.4g}"
 
 
-@pytest.mark.parametrize("dtype,D,L", [c for c in EXACT_CASES if c[0] == torch.bfloat16])
+@pytest.mark.parametrize("dtype,D,L", [c for c in EXACT_CASES if c[0] != torch.float16])
 def test_dropout_exact_mask_dq(dtype, D, L):
     """dQ_i = sum_j P_ij (r Z_ij - Delta_i) K_j with dO . V = 1 and K the key
     code: the query-stationary kernel's mask, element by element."""
@@ -284,27 +287,91 @@ def test_dropout_autograd_and_projected_path():
         _assert16(got[i], ref_g[i], f"from_qkv {NAMES[i]}")
 
 
-def test_dropout_unsupported_configs():
-    """fp32 inputs and sqrt-softmax have no dropout kernels: a clear error,
-    never a silent fallback; p outside [0, 1) is a ValueError."""
-    print("[dropout unsupported]", flush=True)
+def test_dropout_invalid_p_and_eval():
+    """p outside [0, 1) is a ValueError; training=False turns dropout off."""
+    print("[dropout p range]", flush=True)
     m = _m()
     x32 = torch.randn(1, 2, 64, 32, device=DEV)
     cid = torch.zeros(1, 64, dtype=torch.int32, device=DEV)
-    with pytest.raises(m.MpattnUnsupported):
-        m.fused_multi_pathway_attention(x32, x32, x32, x32, x32, x32, None, dropout_p=0.1,
-                                        chain_ids=cid)
     xb = x32.to(torch.bfloat16)
-    with pytest.raises(m.MpattnUnsupported):
-        m.fused_multi_pathway_attention(xb, xb, xb, xb, xb, xb, None, dropout_p=0.1,
-                                        sqrt_softmax=True, chain_ids=cid)
     with pytest.raises(ValueError):
         m.fused_multi_pathway_attention(xb, xb, xb, xb, xb, xb, None, dropout_p=1.0,
                                         chain_ids=cid)
-    # fp32 in eval mode: dropout is off, the call succeeds
-    m.fused_multi_pathway_attention(x32, x32, x32, x32, x32, x32, None, dropout_p=0.1,
-                                    training=False, chain_ids=cid)
+    a = m.fused_multi_pathway_attention(x32, x32, x32, x32, x32, x32, None, dropout_p=0.1,
+                                        training=False, chain_ids=cid)
+    b = m.fused_multi_pathway_attention(x32, x32, x32, x32, x32, x32, None, chain_ids=cid)
     torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def _assert32(got, ref, what):
+    err = np.abs(got - ref)
+    rel = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    assert err.max() <= 1e-4 and rel <= 1e-4, f"{what}: max err {err.max():.3g}, relative {rel:.3g}"
+
+
+@pytest.mark.parametrize("D,L,sqrt", [(16, 200, False), (32, 257, False), (64, 150, False),
+                                      (16, 180, True), (24, 130, True)])
+def test_dropout_fp32(D, L, sqrt):
+    """fp32 inputs with dropout (and with sqrt-softmax): forward and all six
+    gradients against the oracle at the fp32 bound (1e-4 max-abs and
+    relative Frobenius), Q/K N(0, 1) with scale D^-1/2 and dO scaled so the
+    largest gradient RMS is ~1."""
+    print(f"[dropout fp32] D={D} L={L} sqrt={sqrt}", flush=True)
+    B, H, p, seed = 2, 3, 0.2, 99 + D + L
+    rng = np.random.default_rng(D * 1000 + L)
+    xs = [rng.standard_normal((B, H, L, D)).astype(np.float32) for _ in range(6)]
+    cid = multi_chain_ids(rng, B, L, 3)
+    kp = tail_padding(rng, B, L, 0.1)
+    go = rng.standard_normal((B, H, L, D)).astype(np.float32)
+    sel = dict(chain_ids=cid, key_pad=kp, rope=True, scale=D ** -0.5, sqrt_softmax=sqrt,
+               dropout_p=p, dropout_seed=seed)
+    x64 = [x.astype(np.float64) for x in xs]
+    ref_o, _ = orc.mpattn_forward(*x64, **sel)
+    ref = orc.mpattn_backward(*x64, go.astype(np.float64), **sel)
+    f = 2.0 ** -round(np.log2(max(float(np.sqrt(np.mean(r ** 2))) for r in ref)))
+    go = (go * np.float32(f)).astype(np.float32)
+    ref = [r * f for r in ref]
+    m = _m()
+    g = [torch.from_numpy(x).to(DEV) for x in xs]
+    kw = dict(chain_ids=torch.from_numpy(cid).to(DEV), key_padding_mask=torch.from_numpy(kp).to(DEV),
+              rope=True, scale=D ** -0.5, sqrt_softmax=sqrt, dropout_p=p, dropout_seed=seed)
+    out = m.fused_multi_pathway_attention(*g, None, training=True, **kw)
+    grads = m.fused_multi_pathway_attention_bwd(*g, None, torch.from_numpy(go).to(DEV), **kw)
+    torch.cuda.synchronize()
+    _assert32(out.cpu().double().numpy(), ref_o, "out")
+    ref0, _ = orc.mpattn_forward(*x64, **dict(sel, dropout_p=0.0))
+    assert np.abs(ref_o - ref0).max() > 1e-2  # the mask changes the result
+    for name, t, r in zip(NAMES, grads, ref):
+        assert t.dtype == torch.float32
+        _assert32(t.cpu().double().numpy(), r, name)
+
+
+@pytest.mark.parametrize("dtype,D,L", [(torch.bfloat16, 32, 257), (torch.float16, 64, 200),
+                                       (torch.bfloat16, 16, 140)])
+def test_dropout_sqrt_softmax_16bit(dtype, D, L):
+    """Dropout of the sqrt(P) weights (16-bit kernels): forward and
+    gradients against the oracle at the 16-bit bound."""
+    print(f"[dropout sqrt] {dtype} D={D} L={L}", flush=True)
+    B, H, p, seed = 2, 3, 0.25, 7 + D
+    xs, go, cid, kp = _random(B, H, L, D, seed=D + 3 * L)
+    xr = _rounded(xs, dtype)
+    sel = dict(chain_ids=cid, key_pad=kp, rope=True, scale=D ** -0.5, sqrt_softmax=True,
+               dropout_p=p, dropout_seed=seed)
+    ref_o, _ = orc.mpattn_forward(*xr, **sel)
+    ref = orc.mpattn_backward(*xr, _rounded([go], dtype)[0], **sel)
+    m = _m()
+    g = [torch.as_tensor(x).to(dtype).to(DEV) for x in xs]
+    kw = dict(chain_ids=torch.from_numpy(cid).to(DEV), key_padding_mask=torch.from_numpy(kp).to(DEV),
+              rope=True, scale=D ** -0.5, sqrt_softmax=True, dropout_p=p, dropout_seed=seed)
+    out = m.fused_multi_pathway_attention(*g, None, training=True, **kw)
+    grads = m.fused_multi_pathway_attention_bwd(*g, None, torch.as_tensor(go).to(dtype).to(DEV), **kw)
+    torch.cuda.synchronize()
+    _assert16(out.float().cpu().double().numpy(), ref_o, "out")
+    ref0, _ = orc.mpattn_forward(*xr, **dict(sel, dropout_p=0.0))
+    assert np.abs(ref_o - ref0).max() > 0.1  # the mask changes the result
+    for name, t, r in zip(NAMES, grads, ref):
+        _assert16(t.float().cpu().double().numpy(), r, name)
 
 
 def test_dropout_long_rows():
