@@ -22,9 +22,11 @@
 // Launches:
 //  1. bwd_prep_kernel: chain staging for keys (as the forward) and queries,
 //     Delta and LSE*log2(e) per query, RoPE-rotated Q_self/K_self.
-//  2. bwd_dkdv_kernel (key-stationary): each wavefront keeps K and V of 32
-//     keys in registers (MFMA B operands) and streams 64-query stages of
-//     Q_self, Q_multi, dO through LDS. S and dP come out with lane = key and
+//  2. bwd_dkdv_kernel (key-stationary, one pathway per workgroup: a pair
+//     contributes to one pathway only, so a workgroup holds that pathway's
+//     operands and accumulators): each wavefront keeps K and V of 32 keys in
+//     registers (MFMA B operands) and streams 64-query stages of Q (of the
+//     pathway) and dO through LDS. S and dP come out with lane = key and
 //     slot = query (query rows read bit-2/3-swapped), which is directly the A
 //     operand of dV += P^T dO and dK += dS^T Q; dO^T and Q^T are transpose
 //     reads of the row-major tiles.
@@ -275,62 +277,72 @@ __device__ void store_rows(const f32x16* acc, float* scratch, const mpattn_tenso
 // ---------------------------------------------------------------------------
 // dK / dV: key-stationary.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP>
-__global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
+// Stage layout of the dK/dV kernel (one pathway per workgroup): Q of the
+// pathway and dO tiles, the aux rows, and (dense mask) the mask tile.
+template <int D, int W, bool DENSE> struct DkdvStage {
+    using TS = TileShape<D>;
+    static constexpr int NTEN = 2;  // Q of the workgroup's pathway, dO
+    static constexpr int AUX = 4 * kBS * 4;  // lse2, delta, qcid (+ spare) floats/ints
+    // Dense mask: the stage's tile of mask bytes, kBS query rows x the
+    // workgroup's 32 W keys, copied with the stage (when a.mdma).
+    static constexpr int MROW = 32 * W;
+    static constexpr int MSK = DENSE ? kBS * MROW : 0;
+    static constexpr int STAGE = NTEN * TS::TILE + AUX + MSK;
+    // Copies run NBUF-1 stages ahead (three buffers where they fit in 64 KB).
+    static constexpr int NBUF = 3 * STAGE <= 65536 ? 3 : 2;
+    static constexpr int SMEM = NBUF * STAGE > W * 32 * 65 * 4 ? NBUF * STAGE : W * 32 * 65 * 4;
+};
+
+// The gradients of pathway PW for the 32 W keys of key block kblk of (b, h):
+// a (query, key) pair contributes to exactly one pathway, so the workgroup
+// needs that pathway's K / V operands and accumulators only, and its stage
+// tiles hold Q of that pathway and dO.
+template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP, int PW>
+__device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, int kblk, int bh) {
     using TS = TileShape<D>;
     using BS = BwdShape<D>;
     using E = Elt<T>;
+    using SL = DkdvStage<D, W, DENSE>;
     typedef typename E::v8 v8;
     typedef short s4 __attribute__((ext_vector_type(4)));
-    constexpr int NTEN = 3;  // Q_self, Q_multi, dO
+    constexpr int NTEN = SL::NTEN;
     constexpr int TOT = NTEN * TS::NI;
     constexpr int NJ = (TOT + W - 1) / W;  // copies per wave (the last may be idle)
-    constexpr int AUX = 4 * kBS * 4;  // lse2, delta, qcid (+ spare) floats/ints
-    // Dense mask: the stage's tile of mask bytes, kBS query rows x the
-    // workgroup's 32 W keys, copied with the stage (when a.mdma).
-    constexpr int MROW = 32 * W;
-    constexpr int MSK = DENSE ? kBS * MROW : 0;
-    constexpr int STAGE = NTEN * TS::TILE + AUX + MSK;
-    // Copies run NBUF-1 stages ahead (three buffers where they fit in 64 KB).
-    constexpr int NBUF = 3 * STAGE <= 65536 ? 3 : 2;
+    constexpr int AUX = SL::AUX;
+    constexpr int MROW = SL::MROW;
+    constexpr int MSK = SL::MSK;
+    constexpr int STAGE = SL::STAGE;
+    constexpr int NBUF = SL::NBUF;
     static_assert(!DENSE || (kBS * MROW) % (1024 * W) == 0, "mask tile copies split evenly over the waves");
     const mpattn_bwd_params& p = a.p;
-
-    __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE > W * 32 * 65 * 4 ? NBUF * STAGE
-                                                                                   : W * 32 * 65 * 4];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
     const int L = p.L, H = p.H, Lp = a.Lp;
-    const int nkb = (L + 32 * W - 1) / (32 * W);
-    // Key blocks whose keys span two chains or hold padded keys (both take
-    // the two-pathway mode for every query subtile) are dispatched first.
-    int kblk, bh;
-    dispatch_order(nkb, H, DENSE ? nullptr : reinterpret_cast<const int4*>(a.ksum), Lp / 32, (L + 31) / 32, W,
-                   true, (int64_t)3 * L * D * sizeof(T), 2 << 20, kblk, bh);
     const int b = bh / H, h = bh % H;
     const int kw0 = kblk * 32 * W + wave * 32;  // first key of this wave
     const int key = kw0 + ql;                   // this lane's key (B operand column)
 
     auto base = [&](const mpattn_tensor& t) { return (const T*)t.ptr + b * t.stride_b + h * t.stride_h; };
-    const T* const qs_p = ROPE ? (const T*)a.qrot + (int64_t)bh * Lp * D : base(p.q_self);
-    const int64_t qs_t = ROPE ? D : p.q_self.stride_t;
-    const T* const qm_p = ROPE ? (const T*)a.qmf + (int64_t)bh * Lp * D : base(p.q_multi);
-    const int64_t qm_t = ROPE ? D : p.q_multi.stride_t;
+    // Q and K of the pathway (with fused RoPE: the prep kernel's folded,
+    // rotated operands), V of the pathway, dO
+    const T* const q_p = PW == 0 ? (ROPE ? (const T*)a.qrot + (int64_t)bh * Lp * D : base(p.q_self))
+                                 : (ROPE ? (const T*)a.qmf + (int64_t)bh * Lp * D : base(p.q_multi));
+    const int64_t q_t = ROPE ? D : (PW == 0 ? p.q_self.stride_t : p.q_multi.stride_t);
     const T* const do_p = base(p.grad_out);
-    const T* const ks_p = ROPE ? (const T*)a.krot + (int64_t)bh * Lp * D : base(p.k_self);
-    const int64_t ks_t = ROPE ? D : p.k_self.stride_t;
-    const T* const km_p = base(p.k_multi);
-    const T* const vs_p = base(p.v_self);
-    const T* const vm_p = base(p.v_multi);
+    const T* const k_p = PW == 0 ? (ROPE ? (const T*)a.krot + (int64_t)bh * Lp * D : base(p.k_self))
+                                 : base(p.k_multi);
+    const int64_t k_t = PW == 0 ? (ROPE ? D : p.k_self.stride_t) : p.k_multi.stride_t;
+    const T* const v_p = base(PW == 0 ? p.v_self : p.v_multi);
+    const int64_t v_t = PW == 0 ? p.v_self.stride_t : p.v_multi.stride_t;
     const float* const lse2_bh = a.lse2 + (int64_t)bh * Lp;
     const float* const delta_bh = a.delta + (int64_t)bh * Lp;
     const int* const qcid_b = a.qcid + (int64_t)b * Lp;
     const int4* const qsum_b = reinterpret_cast<const int4*>(a.qsum) + (int64_t)b * (Lp / 32);
 
     // ---- key-side registers: B operands K[key][dims kk*16 + 8*hh + (0..7)] ----
-    v8 kf[2][BS::NKK], vf[2][BS::NKK];
+    v8 kf[BS::NKK], vf[BS::NKK];
     const bool kin = key < L;
     // Dense mask tile: the workgroup's first key, and this lane's byte
     // offset in a tile row. The last 16-key chunk that holds keys < L is
@@ -347,17 +359,12 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     for (int kk = 0; kk < BS::NKK; ++kk) {
         const int d0 = kk * 16 + hh * 8;
         float x[8];
-#pragma unroll
-        for (int pw = 0; pw < 2; ++pw) {
-            const T* kr = pw == 0 ? ks_p + (int64_t)key * ks_t : km_p + (int64_t)key * p.k_multi.stride_t;
-            const T* vr = pw == 0 ? vs_p + (int64_t)key * p.v_self.stride_t : vm_p + (int64_t)key * p.v_multi.stride_t;
-            if (kin && d0 < D) load8f<T>(kr, d0, x);
-            else for (int u = 0; u < 8; ++u) x[u] = 0.f;
-            kf[pw][kk] = pack8<T>(x);
-            if (kin && d0 < D) load8f<T>(vr, d0, x);
-            else for (int u = 0; u < 8; ++u) x[u] = 0.f;
-            vf[pw][kk] = pack8<T>(x);
-        }
+        if (kin && d0 < D) load8f<T>(k_p + (int64_t)key * k_t, d0, x);
+        else for (int u = 0; u < 8; ++u) x[u] = 0.f;
+        kf[kk] = pack8<T>(x);
+        if (kin && d0 < D) load8f<T>(v_p + (int64_t)key * v_t, d0, x);
+        else for (int u = 0; u < 8; ++u) x[u] = 0.f;
+        vf[kk] = pack8<T>(x);
     }
     const int ckey = kin ? a.keff[(int64_t)b * Lp + key] : kPadChain;  // kPadChain if padded
     const bool kvalid = ckey != kPadChain;
@@ -368,16 +375,12 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     const uint32_t key_live = (uint32_t)__builtin_amdgcn_ballot_w64(kvalid);
     const bool any_live = key_live != 0;
 
-    // ---- accumulators: [0] self, [1] multimer. Each subtile pass updates
-    // both from one code block (the pathway it does not serve gets zero
-    // operands), so they keep one register home: no copies between passes.
-    f32x16 dv[2][BS::NDB], dk[2][BS::NDB];
+    // ---- accumulators of the workgroup's pathway ----
+    f32x16 dv[BS::NDB], dk[BS::NDB];
 #pragma unroll
-    for (int pw = 0; pw < 2; ++pw)
+    for (int db = 0; db < BS::NDB; ++db)
 #pragma unroll
-        for (int db = 0; db < BS::NDB; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) dv[pw][db][i] = dk[pw][db][i] = 0.f;
+        for (int i = 0; i < 16; ++i) dv[db][i] = dk[db][i] = 0.f;
     // ---- DMA plan (as the forward) ----
     const char* dsb[NJ];
     unsigned dstr[NJ], dlds[NJ], dloff[NJ];
@@ -392,8 +395,8 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
         const int ten = ins / TS::NI, part = ins % TS::NI;
         int r, cb;
         dma_slot(j, r, cb);
-        const T* tb = ten == 0 ? qs_p : ten == 1 ? qm_p : do_p;
-        const int64_t ts = ten == 0 ? qs_t : ten == 1 ? qm_t : p.grad_out.stride_t;
+        const T* tb = ten == 0 ? q_p : do_p;
+        const int64_t ts = ten == 0 ? q_t : p.grad_out.stride_t;
         dsb[j] = (const char*)tb;
         dstr[j] = (unsigned)(ts * (int64_t)sizeof(T));
         dlds[j] = ten * TS::TILE + part * 1024;
@@ -506,12 +509,10 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
         return acc;
     };
 
-    // One pass over a subtile of 32 queries on pathway pw. masked: only the
-    // pairs on pw count (a subtile with queries or keys on several chains
-    // takes one masked pass per pathway); the others get an infinite LSE,
-    // so their probabilities are 0.
-    auto pass = [&](bool masked, auto pw_c, const char* stage, int st, int q0) {
-        constexpr int pw = decltype(pw_c)::value;
+    // One pass over a subtile of 32 queries. masked: only the pairs on PW
+    // count (a subtile with queries or keys on several chains); the others
+    // get an infinite LSE, so their probabilities are 0.
+    auto pass = [&](bool masked, const char* stage, int st, int q0) {
         float l2[16], dl[16];
         aux16(stage, 0, st, l2);
         aux16(stage, 1, st, dl);
@@ -540,16 +541,16 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
                 } else {
                     same = qc[i] == ckey;
                 }
-                if (same != (pw == 0)) l2[i] = INFINITY;
+                if (same != (PW == 0)) l2[i] = INFINITY;
             }
         }
         v8 qa[BS::NKK], doa[BS::NKK], ka[BS::NKK], va[BS::NKK];
 #pragma unroll
         for (int kk = 0; kk < BS::NKK; ++kk) {
-            doa[kk] = rop(stage, 2, st, kk);
-            qa[kk] = rop(stage, pw, st, kk);
-            ka[kk] = pw ? kf[1][kk] : kf[0][kk];
-            va[kk] = pw ? vf[1][kk] : vf[0][kk];
+            doa[kk] = rop(stage, 1, st, kk);
+            qa[kk] = rop(stage, 0, st, kk);
+            ka[kk] = kf[kk];
+            va[kk] = vf[kk];
         }
         const f32x16 sv = mma_kloop(qa, ka);
         const f32x16 dp = mma_kloop(doa, va);
@@ -570,15 +571,14 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
             dsv[i] = dscore(pm, dpi, dl[i]);
             pv[i] = keep ? pm : 0.f;
         }
-        // dV += P^T dO ; dK += dS^T Q for pathway pw, per 16-query chunk cc
-        // (the other pathway's MFMAs take zero operands)
+        // dV += P^T dO ; dK += dS^T Q, per 16-query chunk cc
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
             const v8 p8 = pack8<T>(pv + 8 * cc), ds8 = pack8<T>(dsv + 8 * cc);
 #pragma unroll
             for (int db = 0; db < BS::NDB; ++db) {
-                dv[pw][db] = E::mma(p8, top(stage, 2, st, cc, db), dv[pw][db]);
-                dk[pw][db] = E::mma(ds8, top(stage, pw, st, cc, db), dk[pw][db]);
+                dv[db] = E::mma(p8, top(stage, 1, st, cc, db), dv[db]);
+                dk[db] = E::mma(ds8, top(stage, 0, st, cc, db), dk[db]);
             }
         }
     };
@@ -640,15 +640,12 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
             md2[st] = qmode(__builtin_amdgcn_readlane(qsw.x, i), __builtin_amdgcn_readlane(qsw.y, i),
                             __builtin_amdgcn_readlane(qsw.z, i));
         }
-        // Up to two passes per subtile (one per pathway for mixed ones), from
-        // one instance of the pass code.
-#pragma unroll 1
-        for (int it = 0; it < 4; ++it) {
-            const int st = it >> 1, ps = it & 1;
+        // One pass per subtile with pairs on PW (masked when the subtile
+        // mixes pathways).
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
             const int md = st ? md2[1] : md2[0];
-            if (md == 3 || (ps == 1 && md != 2)) continue;
-            if ((md == 2 ? ps : md) == 0) pass(md == 2, IC<0>{}, stage, st, q0);
-            else pass(md == 2, IC<1>{}, stage, st, q0);
+            if (md == 2 || md == PW) pass(md == 2, stage, st, q0);
         }
         bf = bf + 1 == NBUF ? 0 : bf + 1;
     }
@@ -657,74 +654,86 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
 
     float* scratch = (float*)(smem + wave * 32 * 65 * 4);
     const float vmul = DROP ? a.drop.rkeep : 1.0f;
-    store_rows<T, D, false>(dv[0], scratch, p.dv_self, b, h, kw0, L, vmul, false, nullptr, nullptr, key_live);
-    store_rows<T, D, false>(dv[1], scratch, p.dv_multi, b, h, kw0, L, vmul, false, nullptr, nullptr, key_live);
-    store_rows<T, D, false>(dk[0], scratch, p.dk_self, b, h, kw0, L, a.kmul, ROPE, p.rope_cos, p.rope_sin, key_live);
-    store_rows<T, D, false>(dk[1], scratch, p.dk_multi, b, h, kw0, L, a.kmul, false, nullptr, nullptr, key_live);
+    store_rows<T, D, false>(dv, scratch, PW == 0 ? p.dv_self : p.dv_multi, b, h, kw0, L, vmul, false, nullptr,
+                            nullptr, key_live);
+    store_rows<T, D, false>(dk, scratch, PW == 0 ? p.dk_self : p.dk_multi, b, h, kw0, L, a.kmul, ROPE && PW == 0,
+                            p.rope_cos, p.rope_sin, key_live);
+}
+
+// Workgroup -> (key block, pathway, b*H + h): the two pathways of a key
+// block are neighbours in dispatch order (their K / V and Q tiles share the
+// XCD's L2).
+template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP>
+__global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
+    using SL = DkdvStage<D, W, DENSE>;
+    __shared__ __attribute__((aligned(1024))) char smem[SL::SMEM];
+    const int nkb = (a.p.L + 32 * W - 1) / (32 * W);
+    int blk, bh;
+    dispatch_order(2 * nkb, a.p.H, nullptr, 0, 0, 1, false, (int64_t)3 * a.p.L * D * sizeof(T), 2 << 20, blk, bh);
+    if (blk & 1) dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, blk >> 1, bh);
+    else dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, blk >> 1, bh);
 }
 
 // ---------------------------------------------------------------------------
 // dQ: query-stationary.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP>
-__global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
+// Stage layout of the dQ kernel (one pathway per workgroup): K and V tiles
+// of the pathway.
+template <int D, int W> struct DqStage {
+    static constexpr int NTEN = 2;  // K, V of the workgroup's pathway
+    static constexpr int STAGE = NTEN * TileShape<D>::TILE;
+    static constexpr int NBUF = 2;
+    static constexpr int SMEM = NBUF * STAGE > W * 32 * 65 * 4 ? NBUF * STAGE : W * 32 * 65 * 4;
+};
+
+// dQ of pathway PW for the 32 W queries of query block qblk of (b, h).
+template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP, int PW>
+__device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid)[DqStage<D, W>::NBUF][kBS],
+                                        int qblk, int bh) {
     using TS = TileShape<D>;
     using BS = BwdShape<D>;
     using E = Elt<T>;
+    using SL = DqStage<D, W>;
     typedef typename E::v8 v8;
     typedef short s4 __attribute__((ext_vector_type(4)));
-    constexpr int NTEN = 4;  // K_self, K_multi, V_self, V_multi
+    constexpr int NTEN = SL::NTEN;
     constexpr int TOT = NTEN * TS::NI;
     constexpr int NJ = (TOT + W - 1) / W;  // copies per wave (the last may be idle)
-    constexpr int STAGE = NTEN * TS::TILE;
-    constexpr int NBUF = 2;
+    constexpr int STAGE = SL::STAGE;
     const mpattn_bwd_params& p = a.p;
-
-    __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE > W * 32 * 65 * 4 ? NBUF * STAGE
-                                                                                   : W * 32 * 65 * 4];
-    __shared__ __attribute__((aligned(16))) int scid[W][NBUF][kBS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
     const int L = p.L, H = p.H, Lp = a.Lp;
-    const int nqb = (L + 32 * W - 1) / (32 * W);
-    // Query blocks whose rows span two chains are dispatched first.
-    int qblk, bh;
-    dispatch_order(nqb, H, DENSE ? nullptr : reinterpret_cast<const int4*>(a.qsum), Lp / 32, (L + 31) / 32, W,
-                   false, (int64_t)4 * L * D * sizeof(T), 4 << 20, qblk, bh);
     const int b = bh / H, h = bh % H;
     const int qw0 = qblk * 32 * W + wave * 32;
     const int q = qw0 + ql;
     const bool qin = q < L;
 
     auto base = [&](const mpattn_tensor& t) { return (const T*)t.ptr + b * t.stride_b + h * t.stride_h; };
-    const T* const qs_p = ROPE ? (const T*)a.qrot + (int64_t)bh * Lp * D : base(p.q_self);
-    const int64_t qs_t = ROPE ? D : p.q_self.stride_t;
-    const T* const qm_p = ROPE ? (const T*)a.qmf + (int64_t)bh * Lp * D : base(p.q_multi);
-    const int64_t qm_t = ROPE ? D : p.q_multi.stride_t;
+    const T* const q_p = PW == 0 ? (ROPE ? (const T*)a.qrot + (int64_t)bh * Lp * D : base(p.q_self))
+                                 : (ROPE ? (const T*)a.qmf + (int64_t)bh * Lp * D : base(p.q_multi));
+    const int64_t q_t = ROPE ? D : (PW == 0 ? p.q_self.stride_t : p.q_multi.stride_t);
     const T* const do_p = base(p.grad_out);
-    const T* const ks_p = ROPE ? (const T*)a.krot + (int64_t)bh * Lp * D : base(p.k_self);
-    const int64_t ks_t = ROPE ? D : p.k_self.stride_t;
-    const T* const km_p = base(p.k_multi);
-    const T* const vs_p = base(p.v_self);
-    const T* const vm_p = base(p.v_multi);
+    const T* const k_p = PW == 0 ? (ROPE ? (const T*)a.krot + (int64_t)bh * Lp * D : base(p.k_self))
+                                 : base(p.k_multi);
+    const int64_t k_t = PW == 0 ? (ROPE ? D : p.k_self.stride_t) : p.k_multi.stride_t;
+    const T* const v_p = base(PW == 0 ? p.v_self : p.v_multi);
+    const int64_t v_t = PW == 0 ? p.v_self.stride_t : p.v_multi.stride_t;
     const int* const keff_b = a.keff + (int64_t)b * Lp;
     const int4* const ksum_b = reinterpret_cast<const int4*>(a.ksum) + (int64_t)b * (Lp / 32);
 
     // ---- query-side registers (B operands) ----
-    v8 qf[2][BS::NKK], dof[BS::NKK];
+    v8 qf[BS::NKK], dof[BS::NKK];
 #pragma unroll
     for (int kk = 0; kk < BS::NKK; ++kk) {
         const int d0 = kk * 16 + hh * 8;
         float x[8];
         const bool ok = qin && d0 < D;
-        if (ok) load8f<T>(qs_p + (int64_t)q * qs_t, d0, x);
+        if (ok) load8f<T>(q_p + (int64_t)q * q_t, d0, x);
         else for (int u = 0; u < 8; ++u) x[u] = 0.f;
-        qf[0][kk] = pack8<T>(x);
-        if (ok) load8f<T>(qm_p + (int64_t)q * qm_t, d0, x);
-        else for (int u = 0; u < 8; ++u) x[u] = 0.f;
-        qf[1][kk] = pack8<T>(x);
+        qf[kk] = pack8<T>(x);
         if (ok) load8f<T>(do_p + (int64_t)q * p.grad_out.stride_t, d0, x);
         else for (int u = 0; u < 8; ++u) x[u] = 0.f;
         dof[kk] = pack8<T>(x);
@@ -748,13 +757,11 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
         mrow = p.chain_mask + (int64_t)b * p.mask_stride_b + (int64_t)(qin ? q : 0) * p.mask_stride_q;
     }
 
-    f32x16 dq[2][BS::NDB];
+    f32x16 dq[BS::NDB];
 #pragma unroll
-    for (int pw = 0; pw < 2; ++pw)
+    for (int db = 0; db < BS::NDB; ++db)
 #pragma unroll
-        for (int db = 0; db < BS::NDB; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) dq[pw][db][i] = 0.f;
+        for (int i = 0; i < 16; ++i) dq[db][i] = 0.f;
 
     // ---- DMA plan ----
     const char* dsb[NJ];
@@ -770,9 +777,8 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
         const int ten = ins / TS::NI, part = ins % TS::NI;
         int r, cb;
         dma_slot(j, r, cb);
-        const T* tb = ten == 0 ? ks_p : ten == 1 ? km_p : ten == 2 ? vs_p : vm_p;
-        const int64_t ts = ten == 0 ? ks_t : ten == 1 ? p.k_multi.stride_t : ten == 2 ? p.v_self.stride_t
-                                                                                       : p.v_multi.stride_t;
+        const T* tb = ten == 0 ? k_p : v_p;
+        const int64_t ts = ten == 0 ? k_t : v_t;
         dsb[j] = (const char*)tb;
         dstr[j] = (unsigned)(ts * (int64_t)sizeof(T));
         dlds[j] = ten * TS::TILE + part * 1024;
@@ -852,40 +858,26 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
         return acc;
     };
 
-    // One 32-key subtile; mode 0/1: pure pathway, 2: both pathways.
+    // One 32-key subtile of pathway PW; masked: the subtile mixes pathways
+    // (or holds padded keys), so only its pairs on PW count.
     uint64_t mcur[2][2], mnxt[2][2];  // dense mask words (see mload below)
-    auto subtile = [&](const char* stage, const int* cid, int st, int mode, int k0) {
-        f32x16 dsv;
-        bool same[16];
-        if (mode != 2) {
-            const int pw = mode;
-            v8 ka[BS::NKK], va[BS::NKK];
+    auto subtile = [&](const char* stage, const int* cid, int st, bool masked, int k0) {
+        v8 ka[BS::NKK], va[BS::NKK];
 #pragma unroll
-            for (int kk = 0; kk < BS::NKK; ++kk) {
-                ka[kk] = rop(stage, pw, st, kk);
-                va[kk] = rop(stage, 2 + pw, st, kk);
-            }
-            const f32x16 sv = mma_kloop(ka, pw == 0 ? qf[0] : qf[1]);
-            const f32x16 dp = mma_kloop(va, dof);
+        for (int kk = 0; kk < BS::NKK; ++kk) {
+            ka[kk] = rop(stage, 0, st, kk);
+            va[kk] = rop(stage, 1, st, kk);
+        }
+        const f32x16 sv = mma_kloop(ka, qf);
+        const f32x16 dp = mma_kloop(va, dof);
+        float dsv[16];
+        if (!masked) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const float pv = fast_exp2(fmaf(sv[i], c, -l2));
                 dsv[i] = dscore(pv, dpe(dp[i], k0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8)), dl);
-                same[i] = pw == 0;
             }
         } else {
-            v8 kas[BS::NKK], kam[BS::NKK], vas[BS::NKK], vam[BS::NKK];
-#pragma unroll
-            for (int kk = 0; kk < BS::NKK; ++kk) {
-                kas[kk] = rop(stage, 0, st, kk);
-                kam[kk] = rop(stage, 1, st, kk);
-                vas[kk] = rop(stage, 2, st, kk);
-                vam[kk] = rop(stage, 3, st, kk);
-            }
-            const f32x16 ss = mma_kloop(kas, qf[0]);
-            const f32x16 sm = mma_kloop(kam, qf[1]);
-            const f32x16 dps = mma_kloop(vas, dof);
-            const f32x16 dpm = mma_kloop(vam, dof);
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 const int kl = st * 32 + 16 * cc + 8 * hh;
@@ -903,30 +895,18 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
                     } else {
                         sm_ = ck == cq;
                     }
-                    same[i] = sm_;
-                    const float s = sm_ ? ss[i] : sm[i];
-                    const float dp = sm_ ? dps[i] : dpm[i];
-                    const float pv = ck == kPadChain ? 0.f : fast_exp2(fmaf(s, c, -l2));
-                    dsv[i] = dscore(pv, dpe(dp, k0 + kl + t), dl);
+                    const bool on = ck != kPadChain && sm_ == (PW == 0);
+                    const float pv = on ? fast_exp2(fmaf(sv[i], c, -l2)) : 0.f;
+                    dsv[i] = dscore(pv, dpe(dp[i], k0 + kl + t), dl);
                 }
             }
         }
-        // dQ^T_pw += K_pw^T dS^T
+        // dQ^T += K^T dS^T
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-            v8 dss, dsm;
+            const v8 ds8 = pack8<T>(dsv + 8 * cc);
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const int i = 8 * cc + t;
-                const T dv_ = (T)dsv[i];
-                dss[t] = same[i] ? dv_ : (T)0.f;
-                dsm[t] = same[i] ? (T)0.f : dv_;
-            }
-#pragma unroll
-            for (int db = 0; db < BS::NDB; ++db) {
-                if (mode != 1) dq[0][db] = E::mma(top(stage, 0, st, cc, db), dss, dq[0][db]);
-                if (mode != 0) dq[1][db] = E::mma(top(stage, 1, st, cc, db), dsm, dq[1][db]);
-            }
+            for (int db = 0; db < BS::NDB; ++db) dq[db] = E::mma(top(stage, 0, st, cc, db), ds8, dq[db]);
         }
     };
 
@@ -998,9 +978,8 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
             const int i = 2 * s + st - sub0;
             const int md = kmode(__builtin_amdgcn_readlane(ksw.x, i), __builtin_amdgcn_readlane(ksw.y, i),
                                  __builtin_amdgcn_readlane(ksw.z, i));
-            if (md == 0) subtile(stage, cid, st, 0, k0);
-            else if (md == 1) subtile(stage, cid, st, 1, k0);
-            else if (md == 2) subtile(stage, cid, st, 2, k0);
+            if (md == PW) subtile(stage, cid, st, false, k0);
+            else if (md == 2) subtile(stage, cid, st, true, k0);
         }
         if constexpr (DENSE) {
 #pragma unroll
@@ -1013,9 +992,22 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     stage_barrier();
 
     float* scratch = (float*)(smem + wave * 32 * 65 * 4);
-    const float scale = p.scale;
-    store_rows<T, D, true>(dq[0], scratch, p.dq_self, b, h, qw0, L, scale, ROPE, p.rope_cos, p.rope_sin);
-    store_rows<T, D, true>(dq[1], scratch, p.dq_multi, b, h, qw0, L, scale, false, nullptr, nullptr);
+    store_rows<T, D, true>(dq, scratch, PW == 0 ? p.dq_self : p.dq_multi, b, h, qw0, L, p.scale, ROPE && PW == 0,
+                           p.rope_cos, p.rope_sin);
+}
+
+// Workgroup -> (query block, pathway, b*H + h), the two pathways of a
+// query block neighbours in dispatch order.
+template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP>
+__global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
+    using SL = DqStage<D, W>;
+    __shared__ __attribute__((aligned(1024))) char smem[SL::SMEM];
+    __shared__ __attribute__((aligned(16))) int scid[W][SL::NBUF][kBS];
+    const int nqb = (a.p.L + 32 * W - 1) / (32 * W);
+    int blk, bh;
+    dispatch_order(2 * nqb, a.p.H, nullptr, 0, 0, 1, false, (int64_t)2 * a.p.L * D * sizeof(T), 4 << 20, blk, bh);
+    if (blk & 1) dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, scid, blk >> 1, bh);
+    else dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, scid, blk >> 1, bh);
 }
 
 // ---------------------------------------------------------------------------
@@ -1074,9 +1066,9 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     } else {
     const int nb = (p.L + 32 * W - 1) / (32 * W);
     const unsigned grid = (unsigned)((int64_t)p.B * p.H * nb);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(grid), dim3(W * 64), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(2 * grid), dim3(W * 64), 0, stream, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(grid), dim3(W * 64), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(2 * grid), dim3(W * 64), 0, stream, a);
     return hipGetLastError();
     }
 }
