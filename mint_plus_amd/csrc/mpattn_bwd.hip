@@ -298,7 +298,7 @@ template <int D, int W, bool DENSE> struct DkdvStage {
 // needs that pathway's K / V operands and accumulators only, and its stage
 // tiles hold Q of that pathway and dO.
 template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP, int PW>
-__device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, int kblk, int bh) {
+__device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, uint64_t* wmask, int kblk, int bh) {
     using TS = TileShape<D>;
     using BS = BwdShape<D>;
     using E = Elt<T>;
@@ -613,16 +613,52 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, int kblk
         if (a.mdma)
             for (int m = wave; m < MSK / 1024; m += W) ++ncp;
     }
+    // Stages with work for this workgroup's pathway (some wave has a subtile
+    // whose pairs include pathway PW): up to 64 stages (lane = stage), the
+    // other stages are neither copied nor waited for. Longer rows run every
+    // stage.
+    uint64_t smask = ~0ull;
+    if (nst <= 64) {
+        bool need = false;
+        if (lane < nst) {
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const int sb = 2 * lane + st;
+                int4 v = {0, 0, 32, 0};
+                if (sb < Lp / 32) v = qsum_b[sb];
+                const int md = qmode(v.x, v.y, v.z);
+                need = need || md == 2 || md == PW;
+            }
+        }
+        wmask[wave] = __builtin_amdgcn_ballot_w64(need);
+        __syncthreads();
+        smask = 0;
+#pragma unroll
+        for (int w = 0; w < W; ++w) smask |= wmask[w];
+    }
+    // first stage with work after stage `after` (nst if none)
+    auto next_stage = [&](int after) -> int {
+        const int s1 = after + 1;
+        if (nst > 64) return s1;
+        if (s1 >= nst) return nst;
+        const uint64_t m = smask & (~0ull << s1);
+        return m ? __builtin_ctzll(m) : nst;
+    };
     int sub0 = 0;
     int4 qsw = sum_window(0);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // (compiler-visible) the window has landed
+    int up[NBUF];  // the next NBUF stages with work (nst past the last)
+    up[0] = next_stage(-1);
+#pragma unroll
+    for (int t = 1; t < NBUF; ++t) up[t] = up[t - 1] < nst ? next_stage(up[t - 1]) : nst;
 #pragma unroll
     for (int t = 0; t < NBUF - 1; ++t)
-        if (t < nst) issue(t, t);
+        if (up[t] < nst) issue(up[t], t);
     int bf = 0;
-    for (int s = 0; s < nst; ++s) {
+    while (up[0] < nst) {
+        const int s = up[0];
         // stage s's copies have landed (later stages' may stay in flight)
-        if (NBUF == 3 && s + 1 < nst) wait_vm_var(ncp);
+        if (NBUF == 3 && up[1] < nst) wait_vm_var(ncp);
         else wait_vm<0>();
         stage_barrier();
         if (2 * s - sub0 >= 64) {
@@ -630,7 +666,10 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, int kblk
             qsw = sum_window(sub0);
             __builtin_amdgcn_s_waitcnt(0x0F70);  // (drains the copies in flight too; rare)
         }
-        if (s + NBUF - 1 < nst) issue(s + NBUF - 1, bf == 0 ? NBUF - 1 : bf - 1);
+        if (up[NBUF - 1] < nst) issue(up[NBUF - 1], bf == 0 ? NBUF - 1 : bf - 1);
+#pragma unroll
+        for (int t = 0; t < NBUF - 1; ++t) up[t] = up[t + 1];
+        up[NBUF - 1] = up[NBUF - 2] < nst ? next_stage(up[NBUF - 2]) : nst;
         const char* stage = smem + bf * STAGE;
         const int q0 = s * kBS;
         int md2[2];
@@ -667,11 +706,12 @@ template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     using SL = DkdvStage<D, W, DENSE>;
     __shared__ __attribute__((aligned(1024))) char smem[SL::SMEM];
+    __shared__ uint64_t wmask[W];
     const int nkb = (a.p.L + 32 * W - 1) / (32 * W);
     int blk, bh;
     dispatch_order(2 * nkb, a.p.H, nullptr, 0, 0, 1, false, (int64_t)3 * a.p.L * D * sizeof(T), 2 << 20, blk, bh);
-    if (blk & 1) dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, blk >> 1, bh);
-    else dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, blk >> 1, bh);
+    if (blk & 1) dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, wmask, blk >> 1, bh);
+    else dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, wmask, blk >> 1, bh);
 }
 
 // ---------------------------------------------------------------------------
@@ -689,7 +729,7 @@ template <int D, int W> struct DqStage {
 // dQ of pathway PW for the 32 W queries of query block qblk of (b, h).
 template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP, int PW>
 __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid)[DqStage<D, W>::NBUF][kBS],
-                                        int qblk, int bh) {
+                                        uint64_t* wmask, int qblk, int bh) {
     using TS = TileShape<D>;
     using BS = BwdShape<D>;
     using E = Elt<T>;
@@ -939,7 +979,34 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
                 m[st][cc] = w;
             }
     };
-    if constexpr (DENSE) mload(0, mcur);
+    // Key stages with work for this workgroup's pathway (as in the dK/dV
+    // kernel: up to 64 stages, lane = stage; all-padded key stages have none).
+    uint64_t smask = ~0ull;
+    if (nst <= 64) {
+        bool need = false;
+        if (lane < nst) {
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const int sb = 2 * lane + st;
+                int4 v = {0, 0, 32, 0};
+                if (sb < Lp / 32) v = ksum_b[sb];
+                const int md = kmode(v.x, v.y, v.z);
+                need = need || md == 2 || md == PW;
+            }
+        }
+        wmask[wave] = __builtin_amdgcn_ballot_w64(need);
+        __syncthreads();
+        smask = 0;
+#pragma unroll
+        for (int w = 0; w < W; ++w) smask |= wmask[w];
+    }
+    auto next_stage = [&](int after) -> int {
+        const int s1 = after + 1;
+        if (nst > 64) return s1;
+        if (s1 >= nst) return nst;
+        const uint64_t m = smask & (~0ull << s1);
+        return m ? __builtin_ctzll(m) : nst;
+    };
     // Key summaries of a window of 64 subtiles (32 stages), one per lane,
     // read with readlane (as in the dK/dV kernel).
     auto sum_window = [&](int first) {
@@ -949,27 +1016,24 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
     };
     int sub0 = 0;
     int4 ksw = sum_window(0);
-    issue(0, 0);
-    // Key stages after the last one with a valid key (all padded) are not
-    // run; the first summary window decides (at least stage 0 runs).
-    int nrun = nst;
-    for (int s = 0; s < nrun; ++s) {
-        const int bf = s & 1;
+    int cur = next_stage(-1);
+    int nxt = cur < nst ? next_stage(cur) : nst;
+    if constexpr (DENSE)
+        if (cur < nst) mload(cur, mcur);
+    if (cur < nst) issue(cur, 0);
+    int bf = 0;
+    while (cur < nst) {
+        const int s = cur;
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), compiler-visible
         stage_barrier();
-        if (s == 0 && nst <= 32) {
-            const uint64_t live = __builtin_amdgcn_ballot_w64(ksw.z < 32) &
-                                  (nst >= 32 ? ~0ull : (1ull << (2 * nst)) - 1);
-            nrun = live ? (63 - __builtin_clzll(live)) / 2 + 1 : 1;
-        }
         if (2 * s - sub0 >= 64) {
             sub0 = 2 * s;
             ksw = sum_window(sub0);
             __builtin_amdgcn_s_waitcnt(0x0F70);  // before the next copy is issued
         }
         if constexpr (DENSE)
-            if (s + 1 < nrun) mload(s + 1, mnxt);
-        if (s + 1 < nrun) issue(s + 1, bf ^ 1);
+            if (nxt < nst) mload(nxt, mnxt);
+        if (nxt < nst) issue(nxt, bf ^ 1);
         const char* stage = smem + bf * STAGE;
         const int* cid = &scid[wave][bf][0];
         const int k0 = s * kBS;
@@ -987,6 +1051,9 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) mcur[st][cc] = mnxt[st][cc];
         }
+        cur = nxt;
+        nxt = cur < nst ? next_stage(cur) : nst;
+        bf ^= 1;
     }
     wait_vm<0>();
     stage_barrier();
@@ -1003,11 +1070,12 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     using SL = DqStage<D, W>;
     __shared__ __attribute__((aligned(1024))) char smem[SL::SMEM];
     __shared__ __attribute__((aligned(16))) int scid[W][SL::NBUF][kBS];
+    __shared__ uint64_t wmask[W];
     const int nqb = (a.p.L + 32 * W - 1) / (32 * W);
     int blk, bh;
     dispatch_order(2 * nqb, a.p.H, nullptr, 0, 0, 1, false, (int64_t)2 * a.p.L * D * sizeof(T), 4 << 20, blk, bh);
-    if (blk & 1) dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, scid, blk >> 1, bh);
-    else dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, scid, blk >> 1, bh);
+    if (blk & 1) dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, scid, wmask, blk >> 1, bh);
+    else dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, scid, wmask, blk >> 1, bh);
 }
 
 // ---------------------------------------------------------------------------
