@@ -39,6 +39,9 @@ template <> struct Elt<bf16_t> {
     static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
+    static __device__ __forceinline__ f32x4 mma16(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
     // acc + x[0] + x[1] in fp32 (v_dot2_f32_bf16 against (1, 1)).
     static __device__ __forceinline__ float sum2(v2 x, float acc) {
         const v2 one = {(bf16_t)1.0f, (bf16_t)1.0f};
@@ -56,6 +59,9 @@ template <> struct Elt<fp16_t> {
     typedef fp16x2 v2;
     static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 mma16(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
     static __device__ __forceinline__ float sum2(v2 x, float acc) {
         const v2 one = {(fp16_t)1.0f, (fp16_t)1.0f};

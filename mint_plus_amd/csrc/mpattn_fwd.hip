@@ -727,6 +727,22 @@ void fwd_kernel(const FwdArgs args) {
         return sv;
     };
 
+    // Fast-path row sums on the matrix cores (no dropout, no sqrt-softmax):
+    // v_mfma_f32_16x16x32 with the probabilities as the B operand (lane l:
+    // column l%16, k-group l/16, i.e. query l%32 and key half l/32 of a
+    // 16-key chunk) and a 0/1 selector as A (row m, k-group g: 1 iff m is
+    // 0 or 8 for even g, 4 or 12 for odd g). Output row 4*(l/16) of lane l
+    // (its accumulator slot 0) is then the chunk's sum for query l%32 over
+    // both key halves.
+    constexpr bool MSUM = !SQRT && !DROP;
+    v8 rsel;
+    {
+        const int sm = lane & 15, sg = lane >> 4;
+        const bool one = (sm & 3) == 0 && ((sm >> 2) & 1) == (sg & 1);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) rsel[t] = one ? (T)1.0f : (T)0.0f;
+    }
+
     // Q operands of the fast path's pathway (changes rarely: at chain edges).
     int cur_pw = 0;
     v8 qcur[QB][S::NKK];
@@ -740,33 +756,60 @@ void fwd_kernel(const FwdArgs args) {
     // cores work on block u+1 while the VALU does block u's softmax. Returns
     // the mask of blocks accumulated; a block that needs the fix-up is left
     // to the slow path.
-    auto fast_stage = [&](const char* stage, int pw, int k0) -> int {
-        const char* kt = stage + pw * S::TILE;
-        const char* vt = stage + (2 + pw) * S::TILE;
+    // MIXED: the two subtiles are on different pathways (pw0, pw1: a chain
+    // edge at key 32 of the stage); the Q operands are then selected per
+    // subtile instead of taken from qcur.
+    auto fast_stage = [&](auto mixed_c, const char* stage, int pw0, int pw1, int k0) -> int {
+        constexpr bool MIXED = decltype(mixed_c)::value;
+        const char* const kt[2] = {stage + pw0 * S::TILE, stage + pw1 * S::TILE};
+        const char* const vt[2] = {stage + (2 + pw0) * S::TILE, stage + (2 + pw1) * S::TILE};
         // All LDS operands are read up front: the V reads overlap the softmax.
         v8 ka[2][S::NKK], va[2][2][S::NDB];
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
-            for (int kk = 0; kk < S::NKK; ++kk) ka[st][kk] = kop_t(kt, st, kk);
+            for (int kk = 0; kk < S::NKK; ++kk) ka[st][kk] = kop_t(kt[st], st, kk);
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-                for (int db = 0; db < S::NDB; ++db) va[st][cc][db] = vop_t(vt, st, cc, db);
+                for (int db = 0; db < S::NDB; ++db) va[st][cc][db] = vop_t(vt[st], st, cc, db);
         // keep every LDS read of the stage ahead of the softmax
         __builtin_amdgcn_sched_barrier(0);
         f32x16 sv[QB][2];
 #pragma unroll
         for (int u = 0; u < QB; ++u)
 #pragma unroll
-            for (int st = 0; st < 2; ++st) sv[u][st] = qkq(ka[st], qcur[u]);
+            for (int st = 0; st < 2; ++st) {
+                if constexpr (MIXED) {
+                    v8 qa[S::NKK];
+#pragma unroll
+                    for (int kk = 0; kk < S::NKK; ++kk) qa[kk] = (st ? pw1 : pw0) ? qf[u][1][kk] : qf[u][0][kk];
+                    sv[u][st] = qkq(ka[st], qa);
+                } else {
+                    sv[u][st] = qkq(ka[st], qcur[u]);
+                }
+            }
         int done = 0;
         for_blocks<QB>([&](auto u_c) {
             constexpr int u = decltype(u_c)::value;
             v8 pb[2][2];
-            const float ls = probs(IC<2>{}, sv[u], pb, false, 0.f, k0 + 8 * hh, drow[u]);
+            float ls;
+            if constexpr (MSUM) {
+                // Row sums of the rounded probabilities on the matrix cores
+                // (rsel: selector operand): the full 64-key sum of lane's
+                // query, booked half per lane half like the VALU sums.
+                probs(IC<2>{}, sv[u], pb, false, 0.f, k0 + 8 * hh, drow[u]);
+                f32x4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < 2; ++st)
+#pragma unroll
+                    for (int cc = 0; cc < 2; ++cc) r = E::mma16(rsel, pb[st][cc], r);
+                ls = 0.5f * r[0];
+            } else {
+                ls = probs(IC<2>{}, sv[u], pb, false, 0.f, k0 + 8 * hh, drow[u]);
+            }
             if (needs_fix(ls, l_run[u])) return;
             l_run[u] += ls;
             done |= 1 << u;
@@ -1060,11 +1103,13 @@ void fwd_kernel(const FwdArgs args) {
         }
 
         const char* stage = smem + bf * S::STAGE;
-        bool fast = c0[0] <= 1;
+        bool fast = c0[0] <= 1 && c1[0] <= 1;
 #pragma unroll
-        for (int u = 0; u < QB; ++u) fast = fast && c0[u] == c0[0] && c1[u] == c0[0] && !shifted[u];
+        for (int u = 0; u < QB; ++u) fast = fast && c0[u] == c0[0] && c1[u] == c1[0] && !shifted[u];
         int done = 0;
-        if (fast) {
+        if (fast && c0[0] != c1[0]) {
+            done = fast_stage(IC<1>{}, stage, c0[0], c1[0], s * kBN);
+        } else if (fast) {
             if (c0[0] != cur_pw) {  // rare: kept a branch (not selects on every stage)
                 asm volatile("" ::: "memory");
                 cur_pw = c0[0];
@@ -1073,7 +1118,7 @@ void fwd_kernel(const FwdArgs args) {
 #pragma unroll
                     for (int kk = 0; kk < S::NKK; ++kk) qcur[u][kk] = cur_pw ? qf[u][1][kk] : qf[u][0][kk];
             }
-            done = fast_stage(stage, c0[0], s * kBN);
+            done = fast_stage(IC<0>{}, stage, c0[0], c0[0], s * kBN);
         }
         if (done != (1 << QB) - 1) {
             const int* cid = &scid[wave][bf][0];
