@@ -528,7 +528,8 @@ def bench_attn8m(args, dev):
 def bench_dense(args, dev):
     """The 150M forward (the headline workload) with the chain information
     given as the reference kernel's (B, L, L) bool mask (True = different
-    chains) instead of chain ids, fused RoPE."""
+    chains) instead of chain ids, fused RoPE; also forward + backward at the
+    training shape (B=8) through the same mask."""
     from mint_plus_amd import _lib
     xs, cid, pad = make_workload(dev)
     cm = (cid[:, :, None] != cid[:, None, :]).contiguous()
@@ -540,7 +541,25 @@ def bench_dense(args, dev):
     wall, per = timed(step, args.steps, args.warmup, torch.cuda.current_stream(dev))
     med = statistics.median(per)
     fl = flops_fwd()
+    # forward (saving LSE) + backward at the training shape (B=8) through the
+    # same mask contract
+    b8 = 8
+    x8 = [x[:b8].contiguous() for x in xs]
+    cm8, pad8 = cm[:b8].contiguous(), pad[:b8].contiguous()
+    g = torch.Generator(device="cpu").manual_seed(SEED + 1)
+    go = torch.randn(b8, H, L, D, generator=g).to(torch.bfloat16).to(dev)
+    out8 = torch.empty_like(x8[0])
+    sel = dict(chain_mask=cm8, key_padding_mask=pad8, rope=True, scale=D ** -0.5)
+
+    def step_fb():
+        _, lse = _lib.mpattn_fwd(*x8, need_lse=True, out=out8, **sel)
+        _lib.mpattn_bwd(*x8, out8, lse, go, **sel)
+
+    _, per_fb = timed(step_fb, max(10, args.steps // 2), args.warmup, torch.cuda.current_stream(dev))
+    med_fb = statistics.median(per_fb)
     print(json.dumps({
+        "fwdbwd_b8_ms": round(med_fb, 5),
+        "fwdbwd_b8_tflops": round((flops_fwd(b8) + flops_bwd(b8)) / (med_fb * 1e-3) / 1e12, 2),
         "metric": "multi-pathway attn fwd TFLOP/s (150M shape, dense chain mask, bf16)",
         "value": round(fl / (med * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,

@@ -24,7 +24,7 @@ inline int rup(int x, int m) { return (x + m - 1) / m * m; }
 //                multiplied by the logit factor (so the logits recomputed here
 //                are the ones the forward's LSE was taken over)
 struct BwdWs {
-    int64_t lse2, delta, keff, ksum, qcid, qsum, qrot, krot, qmf, total;
+    int64_t lse2, delta, keff, ksum, qcid, qsum, qrot, krot, qmf, label, valid, total;
 };
 
 inline BwdWs bwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
@@ -41,7 +41,9 @@ inline BwdWs bwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
     const int64_t rot = rope ? (int64_t)B * H * Lp * D * esize : 0;
     w.krot = al(w.qrot + rot);
     w.qmf = al(w.krot + rot);
-    w.total = al(w.qmf + rot);
+    w.label = al(w.qmf + rot);               // dense mask: row labels [B][L]
+    w.valid = al(w.label + (int64_t)B * L * 4);  // dense mask: chain partition per batch row
+    w.total = al(w.valid + (int64_t)B * 4);
     return w;
 }
 
@@ -65,7 +67,19 @@ struct BwdArgs {
     DropCfg drop;
     int mvec;  // dense mask rows readable as aligned 8-byte words
     int mdma;  // dense mask tiles copyable to LDS in 16-byte chunks (dK/dV)
+    // Dense masks: row labels of the mask and per-batch-row flags (1: the
+    // mask is the "different chain" relation of the labels). A launch with
+    // gate set runs only the rows whose flag != 0 equals gate_want.
+    const int* label;
+    const int* gate;
+    int gate_want;
 };
+
+// Row labels of a dense (B, L, L) mask (first key j with mask[b, i, j] == 0)
+// and, with verify, valid[b] = 1 exactly when row b of the mask is the
+// "different chain" relation of its labels (mpattn_fwd.hip).
+hipError_t launch_mask_labels(const uint8_t* mask, int64_t msb, int64_t msq, int64_t msk, int B, int L, int* label,
+                              int* valid, int vec, bool verify, hipStream_t stream);
 
 // fp32 dK/dV and dQ kernels (mpattn_bwd32.hip), run after the prep kernel
 // has filled the workspace that `a` points into.

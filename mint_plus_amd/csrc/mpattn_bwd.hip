@@ -69,7 +69,11 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* l
         if (gid >= p.B * ngrp) return;
         const int b = gid / ngrp, k0 = (gid % ngrp) * 64;
         const int kg = k0 + lane;
-        const int cid = kg < L ? (DENSE ? 0 : p.chain_id[(int64_t)b * L + kg]) : 0;
+        // (dense masks: the row labels for batch rows whose mask is a chain
+        // partition, which run the chain-id kernels; 0 for the others)
+        const int cid = kg >= L ? 0
+                        : !DENSE ? p.chain_id[(int64_t)b * L + kg]
+                        : (a.gate && a.gate[b]) ? a.label[(int64_t)b * L + kg] : 0;
         const bool pad = kg >= L || (p.key_pad && p.key_pad[(int64_t)b * L + kg]);
         const int ke = pad ? kPadChain : cid;
         keff[(int64_t)b * Lp + kg] = ke;
@@ -710,6 +714,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     const int nkb = (a.p.L + 32 * W - 1) / (32 * W);
     int blk, bh;
     dispatch_order(2 * nkb, a.p.H, nullptr, 0, 0, 1, false, (int64_t)3 * a.p.L * D * sizeof(T), 2 << 20, blk, bh);
+    if (a.gate && (a.gate[bh / a.p.H] != 0) != (a.gate_want != 0)) return;  // (uniform)
     if (blk & 1) dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, wmask, blk >> 1, bh);
     else dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, wmask, blk >> 1, bh);
 }
@@ -1074,6 +1079,7 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     const int nqb = (a.p.L + 32 * W - 1) / (32 * W);
     int blk, bh;
     dispatch_order(2 * nqb, a.p.H, nullptr, 0, 0, 1, false, (int64_t)2 * a.p.L * D * sizeof(T), 4 << 20, blk, bh);
+    if (a.gate && (a.gate[bh / a.p.H] != 0) != (a.gate_want != 0)) return;  // (uniform)
     if (blk & 1) dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, scid, wmask, blk >> 1, bh);
     else dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, scid, wmask, blk >> 1, bh);
 }
@@ -1122,18 +1128,46 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
     a.qrot = qrot;
     a.krot = krot;
     a.qmf = qmf;
+    a.label = nullptr;
+    a.gate = nullptr;
+    a.gate_want = 0;
+    hipError_t e;
+    if (DENSE && !F32) {
+        // Row labels of the mask and the check that it is their "different
+        // chain" relation: those batch rows run the chain-id kernels.
+        int* label = (int*)(w + ws.label);
+        int* valid = (int*)(w + ws.valid);
+        if ((e = launch_mask_labels(p.chain_mask, p.mask_stride_b, p.mask_stride_q, p.mask_stride_k, p.B, p.L, label,
+                                    valid, a.mvec, true, stream)) != hipSuccess)
+            return e;
+        a.label = label;
+        a.gate = valid;
+    }
     const int nchain = (p.B * (Lp / 64) + 3) / 4;
     const int nrow = (int)(((int64_t)p.B * p.H * Lp * kPrepLanes<D> + 255) / 256);
     const int nrot = ROPE ? (int)((3 * (int64_t)p.B * p.H * Lp * kRotItems<D> + 255) / 256) : 0;
     hipLaunchKernelGGL((bwd_prep_kernel<T, D, ROPE, DENSE>), dim3(nchain + nrow + nrot), dim3(256), 0, stream,
                        a, lse2, delta, keff, ksum, qcid, qsum, qrot, krot, qmf, nchain, nrow);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     if constexpr (F32) {
         return launch_bwd32(a, stream);
     } else {
     const int nb = (p.L + 32 * W - 1) / (32 * W);
     const unsigned grid = (unsigned)((int64_t)p.B * p.H * nb);
+    if (DENSE) {
+        BwdArgs ac = a;
+        ac.p.chain_id = a.label;
+        ac.p.chain_mask = nullptr;
+        ac.gate_want = 1;
+        hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, false, SQRT, DROP>), dim3(2 * grid), dim3(W * 64), 0,
+                           stream, ac);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, false, SQRT, DROP>), dim3(2 * grid), dim3(W * 64), 0, stream,
+                           ac);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        a.gate_want = 0;
+    }
     hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(2 * grid), dim3(W * 64), 0, stream, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(2 * grid), dim3(W * 64), 0, stream, a);

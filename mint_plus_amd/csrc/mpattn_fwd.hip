@@ -59,8 +59,12 @@ inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 //   qsum int32 [B][Lp/32][4]    queries: min chain, max chain (queries < L), 0, 0
 //   krot T     [B][H][Lp][D]    RoPE-rotated K_self (fused RoPE only)
 //   mcode u8   [B][Lp/32][Lp/32] dense mask: code of each 32 x 32 block
+//   label int32 [B][L]          dense mask: label of each row, the first key
+//                               on its chain (min{j : mask[b, i, j] == 0})
+//   valid int32 [B]             dense mask: 1 when row b of the mask is the
+//                               "different chain" relation of those labels
 struct FwdWs {
-    int64_t keff, ksum, qsum, krot, mcode, total;
+    int64_t keff, ksum, qsum, krot, mcode, label, valid, total;
 };
 
 inline FwdWs fwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
@@ -72,7 +76,9 @@ inline FwdWs fwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
     w.qsum = al(w.ksum + (int64_t)B * (Lp / 32) * 16);
     w.krot = al(w.qsum + (int64_t)B * (Lp / 32) * 16);
     w.mcode = al(w.krot + (rope ? (int64_t)B * H * Lp * D * esize : 0));
-    w.total = al(w.mcode + (int64_t)B * (Lp / 32) * (Lp / 32));
+    w.label = al(w.mcode + (int64_t)B * (Lp / 32) * (Lp / 32));
+    w.valid = al(w.label + (int64_t)B * L * 4);
+    w.total = al(w.valid + (int64_t)B * 4);
     return w;
 }
 
@@ -93,7 +99,91 @@ struct FwdArgs {
     DropCfg drop;  // attention dropout (DROP kernels)
     const uint8_t* mcode;  // dense mask block codes (0 all same chain, 1 all different, 2 mixed)
     int mvec;      // dense mask rows readable as aligned 8-byte words
+    const int* gate;  // per-batch-row flags (dense masks): run only the rows whose
+    int gate_want;    // flag != 0 equals gate_want; null: run every row
 };
+
+// ---------------------------------------------------------------------------
+// Dense masks: row labels. One wavefront per mask row (b, i < L): the label
+// is the first key j with mask[b, i, j] == 0 (the first key on i's chain
+// when the mask is a chain partition; L when the row has none). Also sets
+// valid[b] = 1, which the check below (or the forward's prep kernel, in the
+// same pass as the block codes) clears when a mask entry disagrees.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mask_label_kernel(const uint8_t* mask, int64_t msb, int64_t msq, int64_t msk,
+                                                         int B, int L, int* label, int* valid, int vec) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= (int64_t)B * L) return;
+    const int b = (int)(row / L), i = (int)(row % L);
+    if (i == 0 && lane == 0) valid[b] = 1;
+    const uint8_t* r = mask + (int64_t)b * msb + (int64_t)i * msq;
+    int lab = L;
+    for (int j0 = 0; j0 < L; j0 += 64 * 8) {
+        const int j = j0 + lane * 8;
+        int first = INT32_MAX;
+        if (vec && j + 8 <= L) {
+            const uint64_t w = *reinterpret_cast<const uint64_t*>(r + j);
+#pragma unroll
+            for (int t = 7; t >= 0; --t)
+                if (((w >> (8 * t)) & 0xff) == 0) first = j + t;
+        } else {
+            for (int t = 7; t >= 0; --t)
+                if (j + t < L && r[(int64_t)(j + t) * msk] == 0) first = j + t;
+        }
+        const int m = wave_min_i(first);
+        if (m != INT32_MAX) {
+            lab = m;
+            break;
+        }
+    }
+    if (lane == 0) label[row] = lab;
+}
+
+// Check of a dense mask against its row labels: one wavefront per 32 x 32
+// block (lane: query row lane/2, 16 keys); valid[b] = 0 when some entry
+// with query and key < L differs from (label[q] != label[k]).
+__global__ __launch_bounds__(256) void mask_verify_kernel(const uint8_t* mask, int64_t msb, int64_t msq, int64_t msk,
+                                                          int B, int L, const int* label, int* valid, int vec) {
+    const int lane = threadIdx.x & 63;
+    const int nb = (L + 31) / 32;
+    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= (int64_t)B * nb * nb) return;
+    const int b = (int)(blk / ((int64_t)nb * nb));
+    const int rem = (int)(blk % ((int64_t)nb * nb));
+    const int q = (rem / nb) * 32 + (lane >> 1), k0 = (rem % nb) * 32 + (lane & 1) * 16;
+    bool bad = false;
+    if (q < L) {
+        const uint8_t* row = mask + (int64_t)b * msb + (int64_t)q * msq;
+        const int* lb = label + (int64_t)b * L;
+        const int lq = lb[q];
+        if (vec && k0 + 16 <= L) {
+            const uint64_t w0 = *reinterpret_cast<const uint64_t*>(row + k0);
+            const uint64_t w1 = *reinterpret_cast<const uint64_t*>(row + k0 + 8);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const bool v0 = ((w0 >> (8 * t)) & 0xff) != 0, v1 = ((w1 >> (8 * t)) & 0xff) != 0;
+                bad = bad || v0 != (lb[k0 + t] != lq) || v1 != (lb[k0 + 8 + t] != lq);
+            }
+        } else {
+            for (int t = 0; t < 16; ++t)
+                if (k0 + t < L) bad = bad || (row[(int64_t)(k0 + t) * msk] != 0) != (lb[k0 + t] != lq);
+        }
+    }
+    if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) valid[b] = 0;
+}
+
+hipError_t launch_mask_labels(const uint8_t* mask, int64_t msb, int64_t msq, int64_t msk, int B, int L, int* label,
+                              int* valid, int vec, bool verify, hipStream_t stream) {
+    hipLaunchKernelGGL(mask_label_kernel, dim3((unsigned)(((int64_t)B * L + 3) / 4)), dim3(256), 0, stream, mask, msb,
+                       msq, msk, B, L, label, valid, vec);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !verify) return e;
+    const int64_t nb = (L + 31) / 32;
+    hipLaunchKernelGGL(mask_verify_kernel, dim3((unsigned)((B * nb * nb + 3) / 4)), dim3(256), 0, stream, mask, msb,
+                       msq, msk, B, L, (const int*)label, valid, vec);
+    return hipGetLastError();
+}
 
 // ---------------------------------------------------------------------------
 // Prep: chain staging (blocks [0, nchain)) and K_self rotation (the rest).
@@ -101,7 +191,8 @@ struct FwdArgs {
 template <typename T, int D, bool ROPE, bool DENSE>
 __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p, int* keff,
                                                        int* ksum, int* qsum, T* krot, int Lp, int nchain,
-                                                       uint8_t* mcode, int64_t nrot) {
+                                                       uint8_t* mcode, int64_t nrot, const int* label,
+                                                       int* valid) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int L = p.L;
     if constexpr (DENSE) {
@@ -115,11 +206,15 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p
             const int b = (int)(blk / ((int64_t)nb * nb));
             const int rem = (int)(blk % ((int64_t)nb * nb));
             const int q = (rem / nb) * 32 + (lane >> 1), k0 = (rem % nb) * 32 + (lane & 1) * 16;
-            bool any1 = false, any0 = false;
+            // With row labels, each entry is also checked against them:
+            // mask != 0 exactly when the labels differ.
+            bool any1 = false, any0 = false, bad = false;
             if (q < L) {
                 const uint8_t* row = p.chain_mask + (int64_t)b * p.mask_stride_b + (int64_t)q * p.mask_stride_q;
                 const bool vec = p.mask_stride_k == 1 && ((uintptr_t)p.chain_mask & 7) == 0 &&
                                  (p.mask_stride_b & 7) == 0 && (p.mask_stride_q & 7) == 0;
+                const int* lb = label ? label + (int64_t)b * L : nullptr;
+                const int lq = lb ? lb[q] : 0;
                 if (vec && k0 + 16 <= L) {
                     const uint64_t w0 = *reinterpret_cast<const uint64_t*>(row + k0);
                     const uint64_t w1 = *reinterpret_cast<const uint64_t*>(row + k0 + 8);
@@ -128,6 +223,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p
                         const bool v0 = ((w0 >> (8 * t)) & 0xff) != 0, v1 = ((w1 >> (8 * t)) & 0xff) != 0;
                         any1 = any1 || v0 || v1;
                         any0 = any0 || !v0 || !v1;
+                        if (lb) bad = bad || v0 != (lb[k0 + t] != lq) || v1 != (lb[k0 + 8 + t] != lq);
                     }
                 } else {
                     for (int t = 0; t < 16; ++t)
@@ -135,11 +231,13 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p
                             const bool v = row[(int64_t)(k0 + t) * p.mask_stride_k] != 0;
                             any1 = any1 || v;
                             any0 = any0 || !v;
+                            if (lb) bad = bad || v != (lb[k0 + t] != lq);
                         }
                 }
             }
             const bool a1 = __builtin_amdgcn_ballot_w64(any1) != 0, a0 = __builtin_amdgcn_ballot_w64(any0) != 0;
             if (lane == 0) mcode[blk] = a1 ? (a0 ? 2 : 1) : 0;
+            if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) valid[b] = 0;
             return;
         }
     }
@@ -149,7 +247,8 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p
         if (gid >= p.B * ngrp) return;
         const int b = gid / ngrp, k0 = (gid % ngrp) * 64;
         const int kg = k0 + lane;
-        const int chain = kg < L && !DENSE ? p.chain_id[(int64_t)b * L + kg] : 0;
+        // (dense masks: the row labels stand in for chain ids)
+        const int chain = kg >= L ? 0 : !DENSE ? p.chain_id[(int64_t)b * L + kg] : label ? label[(int64_t)b * L + kg] : 0;
         int cid = kPadChain;
         if (kg < L && !(p.key_pad && p.key_pad[(int64_t)b * L + kg])) cid = chain;
         keff[(int64_t)b * Lp + kg] = cid;
@@ -313,11 +412,21 @@ void fwd_kernel(const FwdArgs args) {
     const int ql = lane & 31, hh = lane >> 5;
     const int L = p.L, H = p.H, Lp = args.Lp;
     const int nqb = (L + QW * W - 1) / (QW * W);
+    // Gated launch (dense masks): a launch with no batch row to run ends
+    // before any other work.
+    if (args.gate) {
+        bool any = false;
+        for (int b0 = 0; b0 < p.B; b0 += 64)
+            any = any || __builtin_amdgcn_ballot_w64(b0 + lane < p.B &&
+                                                     (args.gate[b0 + lane] != 0) == (args.gate_want != 0)) != 0;
+        if (!any) return;
+    }
     // Query blocks whose rows straddle a chain boundary are dispatched first.
     int qb, bh;
     dispatch_order(nqb, H, DENSE ? nullptr : reinterpret_cast<const int4*>(args.qsum), Lp / 32,
                    (L + 31) / 32, QB * W, false, (int64_t)4 * L * D * sizeof(T), 2 << 20, qb, bh);
     const int b = bh / H, h = bh % H;
+    if (args.gate && (args.gate[b] != 0) != (args.gate_want != 0)) return;  // (uniform)
     const int qw0 = qb * QW * W;    // first query of the workgroup
     const int qv0 = qw0 + wave * QW;  // first query of this wavefront
     int qrow[QB];
@@ -1200,13 +1309,39 @@ static hipError_t launch_fwd(FwdArgs& a, hipStream_t stream) {
     const int64_t nrot = ROPE ? ((int64_t)p.B * p.H * Lp * NPC + 255) / 256 : 0;
     uint8_t* mcode = (uint8_t*)(wsb + ws.mcode);
     a.mcode = mcode;
+    a.gate = nullptr;
+    a.gate_want = 0;
+    int* label = DENSE ? (int*)(wsb + ws.label) : nullptr;
+    int* valid = DENSE ? (int*)(wsb + ws.valid) : nullptr;
+    hipError_t e;
+    if (DENSE) {
+        // Row labels of the mask, then (prep kernel) the check that the mask
+        // is the "different chain" relation of those labels.
+        if ((e = launch_mask_labels(p.chain_mask, p.mask_stride_b, p.mask_stride_q, p.mask_stride_k, p.B, p.L, label,
+                                    valid, a.mvec, false, stream)) != hipSuccess)
+            return e;
+    }
     const int64_t nmc = DENSE ? ((int64_t)p.B * (Lp / 32) * (Lp / 32) + 3) / 4 : 0;
     hipLaunchKernelGGL((fwd_prep_kernel<T, D, ROPE, DENSE>), dim3((unsigned)(nchain + nrot + nmc)), dim3(256), 0,
-                       stream, p, keff, ksum, qsum, krot, Lp, nchain, mcode, nrot);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+                       stream, p, keff, ksum, qsum, krot, Lp, nchain, mcode, nrot, (const int*)label, valid);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
     const int nqb = (p.L + 32 * C::QB * C::W - 1) / (32 * C::QB * C::W);
     const int64_t grid = (int64_t)p.B * p.H * nqb;
+    if (DENSE) {
+        // Batch rows whose mask is a chain partition run the chain-id kernel
+        // on the labels (the same pathway for every pair); the others run
+        // the dense-mask kernel. Both launches are gated by valid[b].
+        FwdArgs ac = a;
+        ac.p.chain_id = label;
+        ac.p.chain_mask = nullptr;
+        ac.gate = valid;
+        ac.gate_want = 1;
+        hipLaunchKernelGGL((fwd_kernel<T, D, C::W, C::QB, C::WPE, NBUF, ROPE, false, SQRT, DROP>),
+                           dim3((unsigned)grid), dim3(C::W * 64), 0, stream, ac);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        a.gate = valid;
+        a.gate_want = 0;
+    }
     hipLaunchKernelGGL((fwd_kernel<T, D, C::W, C::QB, C::WPE, NBUF, ROPE, DENSE, SQRT, DROP>), dim3((unsigned)grid),
                        dim3(C::W * 64), 0, stream, a);
     return hipGetLastError();
@@ -1227,10 +1362,12 @@ hipError_t launch_fwd_prep_f32(const mpattn_fwd_params& p, int* keff, int* ksum,
     const int nchain = (p.B * (Lp / 64) + 3) / 4;
     if (p.chain_mask)
         hipLaunchKernelGGL((fwd_prep_kernel<float, 16, false, true>), dim3((unsigned)nchain), dim3(256), 0,
-                           stream, p, keff, ksum, qsum, (float*)nullptr, Lp, nchain, (uint8_t*)nullptr, (int64_t)0);
+                           stream, p, keff, ksum, qsum, (float*)nullptr, Lp, nchain, (uint8_t*)nullptr, (int64_t)0,
+                           (const int*)nullptr, (int*)nullptr);
     else
         hipLaunchKernelGGL((fwd_prep_kernel<float, 16, false, false>), dim3((unsigned)nchain), dim3(256), 0,
-                           stream, p, keff, ksum, qsum, (float*)nullptr, Lp, nchain, (uint8_t*)nullptr, (int64_t)0);
+                           stream, p, keff, ksum, qsum, (float*)nullptr, Lp, nchain, (uint8_t*)nullptr, (int64_t)0,
+                           (const int*)nullptr, (int*)nullptr);
     return hipGetLastError();
 }
 

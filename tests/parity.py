@@ -336,7 +336,7 @@ def _rnd(x, dtype):
     return x.to(dtype).to(torch.float64)
 
 
-def emulate_bwd16(xs, go, cid, kp, rope, scale, dtype, sqrt_softmax=False):
+def emulate_bwd16(xs, go, cid, kp, rope, scale, dtype, sqrt_softmax=False, cross=None):
     """The six gradients computed the way the 16-bit backward kernels round
     (a model of their arithmetic, for calibrating the tests, not an oracle):
     with fused RoPE the logits come from the forward's folded, rounded
@@ -357,8 +357,10 @@ def emulate_bwd16(xs, go, cid, kp, rope, scale, dtype, sqrt_softmax=False):
         qs = _rnd(torch_ref.apply_rope(qs, cos, sin).float().double() * f, dtype) / f
         ks = _rnd(torch_ref.apply_rope(ks, cos, sin).float().double(), dtype)
         qm = _rnd(qm * f, dtype) / f
-    c = torch.from_numpy(cid)
-    cross = (c[:, :, None] != c[:, None, :])[:, None]
+    if cross is None:  # (or a given (B, L, L) "different chain" mask)
+        c = torch.from_numpy(cid)
+        cross = c[:, :, None] != c[:, None, :]
+    cross = torch.as_tensor(cross)[:, None]
     pad = torch.from_numpy(kp)[:, None, None, :]
     s = torch.where(cross, scale * qm @ a[4].transpose(-1, -2), scale * qs @ ks.transpose(-1, -2))
     s = s.masked_fill(pad, float("-inf"))

@@ -74,6 +74,21 @@ def dense_norope_case(D):
     return P.bwd_inputs(2, 2, 200, D, torch.bfloat16, seed=13 + D, go_log2=-2)
 
 
+DENSE_NP = [(300, 32), (200, 64)]
+
+
+def dense_np_case(L, D):
+    """(B=3, H=2) inputs and a (3, L, L) bool mask: row 0 a chain partition,
+    row 1 random (asymmetric), row 2 a partition with one entry flipped."""
+    xs, go, cid, kp = P.bwd_inputs(3, 2, L, D, torch.bfloat16, seed=93 + L + D, nchains=3, go_log2=-2)
+    c = torch.from_numpy(cid)
+    cm = c[:, :, None] != c[:, None, :]
+    g = torch.Generator().manual_seed(L + D + 1)
+    cm[1] = torch.rand(L, L, generator=g) < 0.4
+    cm[2, 5, L - 3] = ~cm[2, 5, L - 3]
+    return xs, go, cm, kp
+
+
 def sqrt_case(D):
     return P.bwd_inputs(2, 2, 140, D, torch.bfloat16, seed=60 + D, go_log2=-4)
 
@@ -205,6 +220,24 @@ def test_bwd_dense_mask_tiles(L, Lpad, D):
     got = [t.float().cpu().numpy().astype(np.float64) for t in grads]
     ref = oracle_grads(xs, go, cid, kp, rope=True, scale=D ** -0.5)
     P.assert_grads16(got, ref, f"dense tiles L={L} Lpad={Lpad}")
+
+
+@pytest.mark.parametrize("L,D", DENSE_NP)
+def test_bwd_dense_mask_not_partition(L, D):
+    """Chain-partition mask rows run the chain-id backward kernels on the
+    mask's row labels, the others the dense-mask kernels, in one call."""
+    print(f"[bwd dense non-partition] L={L} D={D}", flush=True)
+    m = _mpattn()
+    xs, go, cm, kp = dense_np_case(L, D)
+    grads = m.fused_multi_pathway_attention_bwd(*[x.to(DEV) for x in xs], cm.to(DEV), go.to(DEV),
+                                                key_padding_mask=torch.from_numpy(kp).to(DEV), rope=True,
+                                                scale=D ** -0.5)
+    torch.cuda.synchronize()
+    got = [t.float().cpu().numpy().astype(np.float64) for t in grads]
+    a = [x.double().numpy() for x in xs]
+    ref = orc.mpattn_backward(*a, go.double().numpy(), chain_mask=cm.numpy(), key_pad=kp, rope=True,
+                              scale=D ** -0.5)
+    P.assert_grads16(got, ref, f"dense non-partition L={L} D={D}")
 
 
 def test_bwd_fp16():

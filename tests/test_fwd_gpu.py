@@ -54,6 +54,21 @@ def headline_case():
     return P.fwd_inputs(B, H, L, D, torch.bfloat16, seed=2024)
 
 
+DENSE_NP = [(300, 32), (257, 16), (200, 64), (1024, 32)]
+
+
+def dense_np_case(L, D):
+    """(B=3, H=2) inputs and a (3, L, L) bool mask: row 0 a chain partition,
+    row 1 random (asymmetric), row 2 a partition with one entry flipped."""
+    xs, cid, kp = P.fwd_inputs(3, 2, L, D, torch.bfloat16, seed=91 + L + D, nchains=3)
+    c = torch.from_numpy(cid)
+    cm = c[:, :, None] != c[:, None, :]
+    g = torch.Generator().manual_seed(L + D)
+    cm[1] = torch.rand(L, L, generator=g) < 0.4
+    cm[2, 5, L - 3] = ~cm[2, 5, L - 3]
+    return xs, cm, kp
+
+
 def case3b(B, H, L, D):
     return P.fwd_inputs(B, H, L, D, torch.bfloat16, seed=3300 + L, nchains="3b")
 
@@ -178,6 +193,26 @@ def test_fwd_dense_mask_layouts(L, Lpad, D, nchains):
     got = out.float().cpu().numpy().astype(np.float64)
     ref = oracle_out(xs, cid, kp, rope=True, scale=D ** -0.5)
     P.assert16(got, ref, f"dense L={L} Lpad={Lpad} D={D}")
+
+
+@pytest.mark.parametrize("L,D", DENSE_NP)
+def test_fwd_dense_mask_not_partition(L, D):
+    """Dense masks that are not the "different chain" relation of any
+    labelling run the dense-mask kernel; chain-partition masks run the
+    chain-id kernel on the mask's row labels. One batch holds both: row 0 a
+    partition, row 1 a random (asymmetric) mask, row 2 a partition with one
+    entry flipped."""
+    print(f"[fwd dense non-partition] L={L} D={D}", flush=True)
+    m = _mpattn()
+    xs, cm, kp = dense_np_case(L, D)
+    out = m.fused_multi_pathway_attention(*[x.to(DEV) for x in xs], cm.to(DEV), training=False,
+                                          key_padding_mask=torch.from_numpy(kp).to(DEV), rope=True,
+                                          scale=D ** -0.5)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy().astype(np.float64)
+    a = [x.double().numpy() for x in xs]
+    ref, _ = orc.mpattn_forward(*a, chain_mask=cm.numpy(), key_pad=kp, rope=True, scale=D ** -0.5)
+    P.assert16(got, ref, f"dense non-partition L={L} D={D}")
 
 
 def test_fwd_prerotated_contract():

@@ -154,6 +154,26 @@ def test_power_fwd_headline():
     check_fwd_case([x[:1] for x in xs], cid[:1], kp[:1], True, D ** -0.5)
 
 
+@pytest.mark.parametrize("L,D", FW.DENSE_NP[:3])
+def test_power_fwd_dense_not_partition(L, D):
+    xs, cm, kp = FW.dense_np_case(L, D)
+    a = [x.double().numpy() for x in xs]
+    ref, _ = orc.mpattn_forward(*a, chain_mask=cm.numpy(), key_pad=kp, rope=True, scale=D ** -0.5)
+    # a correct kernel's operand rounding passes
+    em, sc = P.round_operands(xs, D, D ** -0.5, True, torch.bfloat16)
+    emo, _ = orc.mpattn_forward(*em, chain_mask=cm.numpy(), key_pad=kp, rope=False, scale=sc)
+    assert P.compare16(emo, ref) is None, P.compare16(emo, ref)
+    # rows 1 and 2 run as if their masks were partitions (labels of the rows)
+    lab = torch.where(~cm, torch.arange(L)[None, None, :], L).amin(dim=2)
+    as_part, _ = orc.mpattn_forward(*a, chain_mask=(lab[:, :, None] != lab[:, None, :]).numpy(),
+                                    key_pad=kp, rope=True, scale=D ** -0.5)
+    bad = {"zero": ref * 0, "half": ref * 0.5, "as_partition": as_part,
+           "swap_v": orc.mpattn_forward(a[0], a[1], a[5], a[3], a[4], a[2], chain_mask=cm.numpy(),
+                                        key_pad=kp, rope=True, scale=D ** -0.5)[0]}
+    passed = [k for k, v in bad.items() if P.compare16(v, ref) is None]
+    assert not passed, f"planted mistakes not rejected: {passed}"
+
+
 @pytest.mark.parametrize("B,H,L,D", FW.CFG3B)
 def test_power_fwd_3b(B, H, L, D):
     xs, cid, kp = FW.case3b(B, H, L, D)
@@ -244,6 +264,31 @@ def test_power_bwd_all_padded_sample():
 def test_power_bwd_fp16():
     xs, go, cid, kp = P.bwd_inputs(2, 3, 190, 32, torch.float16, seed=17)
     check_bwd_case(xs, go, cid, kp, True, 32 ** -0.5, dtype=torch.float16)
+
+
+@pytest.mark.parametrize("L,D", BW.DENSE_NP)
+def test_power_bwd_dense_not_partition(L, D):
+    xs, go, cm, kp = BW.dense_np_case(L, D)
+    a = [x.double().numpy() for x in xs]
+    ref = orc.mpattn_backward(*a, go.double().numpy(), chain_mask=cm.numpy(), key_pad=kp, rope=True,
+                              scale=D ** -0.5)
+    em = P.emulate_bwd16(xs, go, None, kp, True, D ** -0.5, torch.bfloat16, cross=cm)
+    ratio = _worst_ratio(em, ref)
+    assert ratio <= 0.5, f"rounding model uses {ratio:.2f} of the bound"
+    lab = torch.where(~cm, torch.arange(L)[None, None, :], L).amin(dim=2)
+    as_part = orc.mpattn_backward(*a, go.double().numpy(), chain_mask=(lab[:, :, None] != lab[:, None, :]).numpy(),
+                                  key_pad=kp, rope=True, scale=D ** -0.5)
+    names = P.GRAD_NAMES
+    cands = {"as_partition": list(as_part)}
+    for i in (0, 1, 3, 4):
+        g = list(ref)
+        g[i] = g[i] * 0
+        cands[f"zero_{names[i]}"] = g
+    g = list(ref)
+    g[0], g[1], g[3], g[4] = ref[1], ref[0], ref[4], ref[3]
+    cands["swap_dq_dk"] = g
+    passed = [k for k, v in cands.items() if not P.compare_grads16(v, ref)]
+    assert not passed, f"planted mistakes not rejected: {passed}"
 
 
 def test_power_detects_planted_oracle_rope_mistake():
