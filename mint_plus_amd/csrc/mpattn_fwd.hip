@@ -843,7 +843,7 @@ void fwd_kernel(const FwdArgs args) {
     // 0 or 8 for even g, 4 or 12 for odd g). Output row 4*(l/16) of lane l
     // (its accumulator slot 0) is then the chunk's sum for query l%32 over
     // both key halves.
-    constexpr bool MSUM = !SQRT && !DROP;
+    constexpr bool MSUM = !SQRT && !DROP && !DENSE;
     v8 rsel;
     {
         const int sm = lane & 15, sg = lane >> 4;
@@ -1212,11 +1212,13 @@ void fwd_kernel(const FwdArgs args) {
         }
 
         const char* stage = smem + bf * S::STAGE;
-        bool fast = c0[0] <= 1 && c1[0] <= 1;
+        // (dense-mask kernels: both subtiles on one pathway, no mixed stage,
+        // which would not fit their register budget)
+        bool fast = c0[0] <= 1 && c1[0] <= 1 && (!DENSE || c1[0] == c0[0]);
 #pragma unroll
         for (int u = 0; u < QB; ++u) fast = fast && c0[u] == c0[0] && c1[u] == c1[0] && !shifted[u];
         int done = 0;
-        if (fast && c0[0] != c1[0]) {
+        if (!DENSE && fast && c0[0] != c1[0]) {
             done = fast_stage(IC<1>{}, stage, c0[0], c1[0], s * kBN);
         } else if (fast) {
             if (c0[0] != cur_pw) {  // rare: kept a branch (not selects on every stage)
