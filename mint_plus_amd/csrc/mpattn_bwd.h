@@ -42,8 +42,8 @@ inline BwdWs bwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
     w.krot = al(w.qrot + rot);
     w.qmf = al(w.krot + rot);
     w.label = al(w.qmf + rot);               // dense mask: row labels [B][L]
-    w.valid = al(w.label + (int64_t)B * L * 4);  // dense mask: chain partition per batch row
-    w.total = al(w.valid + (int64_t)B * 4);
+    w.valid = al(w.label + (int64_t)B * L * 4);  // dense mask: chain partition per batch row, then any row not
+    w.total = al(w.valid + (int64_t)(B + 1) * 4);
     return w;
 }
 
@@ -68,8 +68,9 @@ struct BwdArgs {
     int mvec;  // dense mask rows readable as aligned 8-byte words
     int mdma;  // dense mask tiles copyable to LDS in 16-byte chunks (dK/dV)
     // Dense masks: row labels of the mask and per-batch-row flags (1: the
-    // mask is the "different chain" relation of the labels). A launch with
-    // gate set runs only the rows whose flag != 0 equals gate_want.
+    // mask is the "different chain" relation of the labels; gate[B] != 0
+    // when some row is not). A launch with gate set runs only the rows whose
+    // flag != 0 equals gate_want.
     const int* label;
     const int* gate;
     int gate_want;
@@ -77,7 +78,8 @@ struct BwdArgs {
 
 // Row labels of a dense (B, L, L) mask (first key j with mask[b, i, j] == 0)
 // and, with verify, valid[b] = 1 exactly when row b of the mask is the
-// "different chain" relation of its labels (mpattn_fwd.hip).
+// "different chain" relation of its labels, valid[B] = 1 when some row is
+// not (valid holds B + 1 ints; mpattn_fwd.hip).
 hipError_t launch_mask_labels(const uint8_t* mask, int64_t msb, int64_t msq, int64_t msk, int B, int L, int* label,
                               int* valid, int vec, bool verify, hipStream_t stream);
 

@@ -714,7 +714,9 @@ __global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
     const int nkb = (a.p.L + 32 * W - 1) / (32 * W);
     int blk, bh;
     dispatch_order(2 * nkb, a.p.H, nullptr, 0, 0, 1, false, (int64_t)3 * a.p.L * D * sizeof(T), 2 << 20, blk, bh);
-    if (a.gate && (a.gate[bh / a.p.H] != 0) != (a.gate_want != 0)) return;  // (uniform)
+    if (a.gate && ((a.gate_want == 0 && a.gate[a.p.B] == 0) ||  // (every row a partition)
+                   (a.gate[bh / a.p.H] != 0) != (a.gate_want != 0)))
+        return;  // (uniform)
     if (blk & 1) dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, wmask, blk >> 1, bh);
     else dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, wmask, blk >> 1, bh);
 }
@@ -1079,7 +1081,9 @@ __global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
     const int nqb = (a.p.L + 32 * W - 1) / (32 * W);
     int blk, bh;
     dispatch_order(2 * nqb, a.p.H, nullptr, 0, 0, 1, false, (int64_t)2 * a.p.L * D * sizeof(T), 4 << 20, blk, bh);
-    if (a.gate && (a.gate[bh / a.p.H] != 0) != (a.gate_want != 0)) return;  // (uniform)
+    if (a.gate && ((a.gate_want == 0 && a.gate[a.p.B] == 0) ||  // (every row a partition)
+                   (a.gate[bh / a.p.H] != 0) != (a.gate_want != 0)))
+        return;  // (uniform)
     if (blk & 1) dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, scid, wmask, blk >> 1, bh);
     else dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, scid, wmask, blk >> 1, bh);
 }

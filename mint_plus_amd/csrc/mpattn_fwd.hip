@@ -61,8 +61,9 @@ inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 //   mcode u8   [B][Lp/32][Lp/32] dense mask: code of each 32 x 32 block
 //   label int32 [B][L]          dense mask: label of each row, the first key
 //                               on its chain (min{j : mask[b, i, j] == 0})
-//   valid int32 [B]             dense mask: 1 when row b of the mask is the
-//                               "different chain" relation of those labels
+//   valid int32 [B + 1]         dense mask: 1 when row b of the mask is the
+//                               "different chain" relation of those labels;
+//                               valid[B] = 1 when some row is not
 struct FwdWs {
     int64_t keff, ksum, qsum, krot, mcode, label, valid, total;
 };
@@ -78,7 +79,7 @@ inline FwdWs fwd_ws_layout(int B, int H, int L, int D, int esize, bool rope) {
     w.mcode = al(w.krot + (rope ? (int64_t)B * H * Lp * D * esize : 0));
     w.label = al(w.mcode + (int64_t)B * (Lp / 32) * (Lp / 32));
     w.valid = al(w.label + (int64_t)B * L * 4);
-    w.total = al(w.valid + (int64_t)B * 4);
+    w.total = al(w.valid + (int64_t)(B + 1) * 4);
     return w;
 }
 
@@ -100,7 +101,8 @@ struct FwdArgs {
     const uint8_t* mcode;  // dense mask block codes (0 all same chain, 1 all different, 2 mixed)
     int mvec;      // dense mask rows readable as aligned 8-byte words
     const int* gate;  // per-batch-row flags (dense masks): run only the rows whose
-    int gate_want;    // flag != 0 equals gate_want; null: run every row
+    int gate_want;    // flag != 0 equals gate_want; null: run every row. With
+                      // gate_want == 0, gate[B] != 0 says that some row runs.
 };
 
 // ---------------------------------------------------------------------------
@@ -116,7 +118,10 @@ __global__ __launch_bounds__(256) void mask_label_kernel(const uint8_t* mask, in
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= (int64_t)B * L) return;
     const int b = (int)(row / L), i = (int)(row % L);
-    if (i == 0 && lane == 0) valid[b] = 1;
+    if (i == 0 && lane == 0) {
+        valid[b] = 1;
+        if (b == 0) valid[B] = 0;
+    }
     const uint8_t* r = mask + (int64_t)b * msb + (int64_t)i * msq;
     int lab = L;
     for (int j0 = 0; j0 < L; j0 += 64 * 8) {
@@ -170,7 +175,10 @@ __global__ __launch_bounds__(256) void mask_verify_kernel(const uint8_t* mask, i
                 if (k0 + t < L) bad = bad || (row[(int64_t)(k0 + t) * msk] != 0) != (lb[k0 + t] != lq);
         }
     }
-    if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) valid[b] = 0;
+    if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) {
+        valid[b] = 0;
+        valid[B] = 1;
+    }
 }
 
 hipError_t launch_mask_labels(const uint8_t* mask, int64_t msb, int64_t msq, int64_t msk, int B, int L, int* label,
@@ -237,7 +245,10 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(const mpattn_fwd_params p
             }
             const bool a1 = __builtin_amdgcn_ballot_w64(any1) != 0, a0 = __builtin_amdgcn_ballot_w64(any0) != 0;
             if (lane == 0) mcode[blk] = a1 ? (a0 ? 2 : 1) : 0;
-            if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) valid[b] = 0;
+            if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) {
+                valid[b] = 0;
+                valid[p.B] = 1;
+            }
             return;
         }
     }
@@ -415,11 +426,14 @@ void fwd_kernel(const FwdArgs args) {
     // Gated launch (dense masks): a launch with no batch row to run ends
     // before any other work.
     if (args.gate) {
-        bool any = false;
-        for (int b0 = 0; b0 < p.B; b0 += 64)
-            any = any || __builtin_amdgcn_ballot_w64(b0 + lane < p.B &&
-                                                     (args.gate[b0 + lane] != 0) == (args.gate_want != 0)) != 0;
-        if (!any) return;
+        if (args.gate_want == 0) {
+            if (args.gate[p.B] == 0) return;  // every row is a partition (one scalar load)
+        } else {
+            bool any = false;
+            for (int b0 = 0; b0 < p.B; b0 += 64)
+                any = any || __builtin_amdgcn_ballot_w64(b0 + lane < p.B && args.gate[b0 + lane] != 0) != 0;
+            if (!any) return;
+        }
     }
     // Query blocks whose rows straddle a chain boundary are dispatched first.
     int qb, bh;

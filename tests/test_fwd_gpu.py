@@ -195,23 +195,29 @@ def test_fwd_dense_mask_layouts(L, Lpad, D, nchains):
     P.assert16(got, ref, f"dense L={L} Lpad={Lpad} D={D}")
 
 
-@pytest.mark.parametrize("L,D", DENSE_NP)
-def test_fwd_dense_mask_not_partition(L, D):
+@pytest.mark.parametrize("L,D,transposed", [c + (False,) for c in DENSE_NP] + [(300, 32, True)])
+def test_fwd_dense_mask_not_partition(L, D, transposed):
     """Dense masks that are not the "different chain" relation of any
     labelling run the dense-mask kernel; chain-partition masks run the
     chain-id kernel on the mask's row labels. One batch holds both: row 0 a
     partition, row 1 a random (asymmetric) mask, row 2 a partition with one
-    entry flipped."""
-    print(f"[fwd dense non-partition] L={L} D={D}", flush=True)
+    entry flipped. ``transposed``: the mask is a transposed view (key stride
+    L, byte loads in the label and check kernels)."""
+    print(f"[fwd dense non-partition] L={L} D={D} transposed={transposed}", flush=True)
     m = _mpattn()
     xs, cm, kp = dense_np_case(L, D)
-    out = m.fused_multi_pathway_attention(*[x.to(DEV) for x in xs], cm.to(DEV), training=False,
+    if transposed:
+        cm = cm.transpose(1, 2)
+    cmd = cm.to(DEV) if not transposed else cm.contiguous().to(DEV).transpose(1, 2).contiguous().transpose(1, 2)
+    if transposed:
+        assert cmd.stride(2) == L
+    out = m.fused_multi_pathway_attention(*[x.to(DEV) for x in xs], cmd, training=False,
                                           key_padding_mask=torch.from_numpy(kp).to(DEV), rope=True,
                                           scale=D ** -0.5)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy().astype(np.float64)
     a = [x.double().numpy() for x in xs]
-    ref, _ = orc.mpattn_forward(*a, chain_mask=cm.numpy(), key_pad=kp, rope=True, scale=D ** -0.5)
+    ref, _ = orc.mpattn_forward(*a, chain_mask=cm.contiguous().numpy(), key_pad=kp, rope=True, scale=D ** -0.5)
     P.assert16(got, ref, f"dense non-partition L={L} D={D}")
 
 
