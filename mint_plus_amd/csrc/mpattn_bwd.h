@@ -12,8 +12,9 @@ constexpr int kBS = 64;  // rows per LDS stage
 inline int rup(int x, int m) { return (x + m - 1) / m * m; }
 
 // Workspace layout (offsets 256-byte aligned), Lp = L rounded up to 64:
-//   lse2  f32   [B][H][Lp]   LSE * log2(e); +inf past L
-//   delta f32   [B][H][Lp]   dO . O; 0 past L
+//   lse2  f32   [B][H][Lp]   -LSE * log2(e); -inf past L (negated: the dK/dV
+//                            kernel starts its S accumulators from it)
+//   delta f32   [B][H][Lp]   -(dO . O); 0 past L (negated, likewise for dP)
 //   keff  int32 [B][Lp]      key chain id, kPadChain for padded / past L
 //   ksum  int32 [B][Lp/32][4] key blocks: min, max chain (valid keys), #padded
 //   qcid  int32 [B][Lp]      query chain id (queries past L: 0)

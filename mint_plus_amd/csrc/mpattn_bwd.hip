@@ -138,8 +138,10 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* l
                 // A row whose keys are all padded has LSE = -inf and no probabilities.
                 l2 = lse == -INFINITY ? INFINITY : lse * a.lmul;
             }
-            lse2[row] = l2;
-            delta[row] = dl;
+            // stored negated: the key-stationary kernel starts its S and dP
+            // accumulators from them (P = exp2(S' ), dS = P dP')
+            lse2[row] = -l2;
+            delta[row] = -dl;
         }
         return;
     }
@@ -211,9 +213,9 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdArgs a, float* l
 //   softmax:       dS = P (dP - delta)
 //   sqrt-softmax:  dS = W dW / 2 - P delta / 2 = W (dW - W delta) / 2
 template <bool SQRT>
-__device__ __forceinline__ float dscore_t(float w, float dw, float delta) {
-    if constexpr (SQRT) return 0.5f * w * (dw - w * delta);
-    return w * (dw - delta);
+__device__ __forceinline__ float dscore_t(float w, float dw, float ndelta) {
+    if constexpr (SQRT) return 0.5f * w * fmaf(w, ndelta, dw);
+    return w * (dw + ndelta);
 }
 
 // Shapes shared by the two gradient kernels.
@@ -503,7 +505,7 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, uint64_t
     };
 
     const float c = a.c;
-    auto dscore = [](float w, float dw, float delta) { return dscore_t<SQRT>(w, dw, delta); };
+    auto dscore = [](float w, float dw, float ndelta) { return dscore_t<SQRT>(w, dw, ndelta); };
     auto mma_kloop = [&](const v8* aop, const v8* bop) {
         f32x16 acc;
 #pragma unroll
@@ -512,12 +514,23 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, uint64_t
         for (int kk = 0; kk < BS::NKK; ++kk) acc = E::mma(aop[kk], bop[kk], acc);
         return acc;
     };
+    // The same product accumulated onto acc0.
+    auto mma_kloop_c = [&](const v8* aop, const v8* bop, f32x16 acc) {
+#pragma unroll
+        for (int kk = 0; kk < BS::NKK; ++kk) acc = E::mma(aop[kk], bop[kk], acc);
+        return acc;
+    };
+    // With fused RoPE the logit factor is folded into Q (c = 1), so without
+    // sqrt-softmax and dropout the accumulators of S and dP start from the
+    // slots' -LSE2 and -Delta: P = exp2(S') and dS = P * dP' need no VALU
+    // work besides the exp2 and one multiply.
+    constexpr bool FOLDC = ROPE && !SQRT && !DROP;
 
     // One pass over a subtile of 32 queries. masked: only the pairs on PW
     // count (a subtile with queries or keys on several chains); the others
     // get an infinite LSE, so their probabilities are 0.
     auto pass = [&](bool masked, const char* stage, int st, int q0) {
-        float l2[16], dl[16];
+        float l2[16], dl[16];  // -LSE2 and -Delta of the slots' queries
         aux16(stage, 0, st, l2);
         aux16(stage, 1, st, dl);
         if (masked) {
@@ -545,7 +558,7 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, uint64_t
                 } else {
                     same = qc[i] == ckey;
                 }
-                if (same != (PW == 0)) l2[i] = INFINITY;
+                if (same != (PW == 0)) l2[i] = -INFINITY;
             }
         }
         v8 qa[BS::NKK], doa[BS::NKK], ka[BS::NKK], va[BS::NKK];
@@ -556,14 +569,29 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, uint64_t
             ka[kk] = kf[kk];
             va[kk] = vf[kk];
         }
+        float pv[16], dsv[16];
+        if constexpr (FOLDC) {
+            f32x16 a0, a1;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                a0[i] = l2[i];
+                a1[i] = dl[i];
+            }
+            const f32x16 sv = mma_kloop_c(qa, ka, a0);   // S - LSE2
+            const f32x16 dp = mma_kloop_c(doa, va, a1);  // dP - Delta
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                pv[i] = fast_exp2(sv[i]);
+                dsv[i] = pv[i] * dp[i];
+            }
+        } else {
         const f32x16 sv = mma_kloop(qa, ka);
         const f32x16 dp = mma_kloop(doa, va);
         // Dropout: dP of dropped entries is 0, kept ones scaled by 1/(1-p);
         // the dV operand is Z*P (the 1/(1-p) goes into the dV store).
-        float pv[16], dsv[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float pm = fast_exp2(fmaf(sv[i], c, -l2[i]));
+            const float pm = fast_exp2(fmaf(sv[i], c, l2[i]));
             float dpi = dp[i];
             bool keep = true;
             if constexpr (DROP) {
@@ -574,6 +602,7 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, uint64_t
             }
             dsv[i] = dscore(pm, dpi, dl[i]);
             pv[i] = keep ? pm : 0.f;
+        }
         }
         // dV += P^T dO ; dK += dS^T Q, per 16-query chunk cc
 #pragma unroll
@@ -785,7 +814,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
         else for (int u = 0; u < 8; ++u) x[u] = 0.f;
         dof[kk] = pack8<T>(x);
     }
-    const float l2 = qin ? a.lse2[(int64_t)bh * Lp + q] : INFINITY;
+    const float l2 = qin ? a.lse2[(int64_t)bh * Lp + q] : -INFINITY;  // -LSE2
     const uint32_t drow = DROP ? drop_row(a.drop.lo, (uint32_t)bh, (uint32_t)q) : 0u;
     // dP of dropped entries is 0, kept ones scaled by 1/(1-p); key of slot i
     // of subtile st: k0 + st*32 + 16*(i/8) + 8*hh + i%8.
@@ -793,7 +822,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
         if constexpr (!DROP) return dp;
         return drop_keep(drow, a.drop.hi, (uint32_t)kg, a.drop.thr) ? dp * a.drop.rkeep : 0.f;
     };
-    const float dl = qin ? a.delta[(int64_t)bh * Lp + q] : 0.f;
+    const float dl = qin ? a.delta[(int64_t)bh * Lp + q] : 0.f;  // -Delta
     int cq = 0, cq_min = 0, cq_max = 0;
     const uint8_t* mrow = nullptr;
     if constexpr (!DENSE) {
@@ -921,7 +950,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
         if (!masked) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float pv = fast_exp2(fmaf(sv[i], c, -l2));
+                const float pv = fast_exp2(fmaf(sv[i], c, l2));
                 dsv[i] = dscore(pv, dpe(dp[i], k0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8)), dl);
             }
         } else {
@@ -943,7 +972,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
                         sm_ = ck == cq;
                     }
                     const bool on = ck != kPadChain && sm_ == (PW == 0);
-                    const float pv = on ? fast_exp2(fmaf(sv[i], c, -l2)) : 0.f;
+                    const float pv = on ? fast_exp2(fmaf(sv[i], c, l2)) : 0.f;
                     dsv[i] = dscore(pv, dpe(dp[i], k0 + kl + t), dl);
                 }
             }

@@ -259,7 +259,7 @@ __device__ void dkdv32_body(const BwdArgs& a, float* smem, int* sint, int kb, in
                 }
                 const float l2 = __int_as_float(si[ql]);
                 const float dl = __int_as_float(si[kTB + ql]);
-                const float pr = on ? fast_exp2(s[i] * c - l2) : 0.f;
+                const float pr = on ? fast_exp2(s[i] * c + l2) : 0.f;  // (l2, dl: -LSE2, -Delta)
                 const float w = SQRT ? sqrtf(pr) : pr;
                 float dpi = dp[i];
                 bool keep = true;
@@ -269,7 +269,7 @@ __device__ void dkdv32_body(const BwdArgs& a, float* smem, int* sint, int kb, in
                     dpi = keep ? dpi * a.drop.rkeep : 0.f;
                 }
                 wv[i] = keep ? w : 0.f;  // (1 / (1 - p) applied when dV is stored)
-                ds[i] = SQRT ? 0.5f * w * (dpi - w * dl) : w * (dpi - dl);
+                ds[i] = SQRT ? 0.5f * w * (dpi + w * dl) : w * (dpi + dl);
             }
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
@@ -336,7 +336,7 @@ __device__ void dq32_body(const BwdArgs& a, float* smem, int* sint, int qb, int 
         gf[kk] = qvalid ? gsrc.base[q * gsrc.st + 2 * kk + hh] : 0.f;
     }
     const int64_t rowi = ((int64_t)b * H + h) * Lp + (qvalid ? q : 0);
-    const float l2 = qvalid ? a.lse2[rowi] : INFINITY;
+    const float l2 = qvalid ? a.lse2[rowi] : -INFINITY;  // -LSE2
     const float dl = qvalid ? a.delta[rowi] : 0.f;
     const uint32_t drow = DROP ? drop_row(a.drop.lo, (uint32_t)(b * H + h), (uint32_t)q) : 0u;
     const int cq = qvalid ? a.qcid[(int64_t)b * Lp + q] : 0;
@@ -409,12 +409,12 @@ __device__ void dq32_body(const BwdArgs& a, float* smem, int* sint, int qb, int 
                     }
                     on = ck != kPadChain && (same == (PW == 0));
                 }
-                const float pr = on ? fast_exp2(s[i] * c - l2) : 0.f;
+                const float pr = on ? fast_exp2(s[i] * c + l2) : 0.f;  // (l2, dl: -LSE2, -Delta)
                 const float w = SQRT ? sqrtf(pr) : pr;
                 float dpi = dp[i];
                 if constexpr (DROP)
                     dpi = drop_keep(drow, a.drop.hi, (uint32_t)(t * kTB + kl), a.drop.thr) ? dpi * a.drop.rkeep : 0.f;
-                ds[i] = SQRT ? 0.5f * w * (dpi - w * dl) : w * (dpi - dl);
+                ds[i] = SQRT ? 0.5f * w * (dpi + w * dl) : w * (dpi + dl);
             }
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
