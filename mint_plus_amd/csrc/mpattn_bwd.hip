@@ -924,7 +924,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
         return db * 32 + (lane & 31) < D ? r8 : zero8;
     };
     const float c = a.c;
-    auto dscore = [](float w, float dw, float delta) { return dscore_t<SQRT>(w, dw, delta); };
+    auto dscore = [](float w, float dw, float ndelta) { return dscore_t<SQRT>(w, dw, ndelta); };
     auto mma_kloop = [&](const v8* aop, const v8* bop) {
         f32x16 acc;
 #pragma unroll
@@ -933,6 +933,24 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
         for (int kk = 0; kk < BS::NKK; ++kk) acc = E::mma(aop[kk], bop[kk], acc);
         return acc;
     };
+    // With fused RoPE (logit factor folded into Q, c = 1), no sqrt-softmax
+    // and no dropout, the S accumulators start from the query's -LSE2
+    // (loop-invariant, the lane's query): P = exp2(S').
+    constexpr bool FOLDC = ROPE && !SQRT && !DROP;
+    f32x16 nl2v;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) nl2v[i] = l2;
+    auto s_of = [&](const v8* aop, const v8* bop) {
+        if constexpr (FOLDC) {
+            f32x16 acc = nl2v;
+#pragma unroll
+            for (int kk = 0; kk < BS::NKK; ++kk) acc = E::mma(aop[kk], bop[kk], acc);
+            return acc;
+        }
+        return mma_kloop(aop, bop);
+    };
+    // probability of slot value x of S (or S' when folded)
+    auto prob = [&](float x) { return FOLDC ? fast_exp2(x) : fast_exp2(fmaf(x, c, l2)); };
 
     // One 32-key subtile of pathway PW; masked: the subtile mixes pathways
     // (or holds padded keys), so only its pairs on PW count.
@@ -944,13 +962,13 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
             ka[kk] = rop(stage, 0, st, kk);
             va[kk] = rop(stage, 1, st, kk);
         }
-        const f32x16 sv = mma_kloop(ka, qf);
+        const f32x16 sv = s_of(ka, qf);
         const f32x16 dp = mma_kloop(va, dof);
         float dsv[16];
         if (!masked) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float pv = fast_exp2(fmaf(sv[i], c, l2));
+                const float pv = prob(sv[i]);
                 dsv[i] = dscore(pv, dpe(dp[i], k0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8)), dl);
             }
         } else {
@@ -972,7 +990,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
                         sm_ = ck == cq;
                     }
                     const bool on = ck != kPadChain && sm_ == (PW == 0);
-                    const float pv = on ? fast_exp2(fmaf(sv[i], c, l2)) : 0.f;
+                    const float pv = on ? prob(sv[i]) : 0.f;
                     dsv[i] = dscore(pv, dpe(dp[i], k0 + kl + t), dl);
                 }
             }
