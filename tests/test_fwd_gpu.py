@@ -221,6 +221,29 @@ def test_fwd_dense_mask_not_partition(L, D, transposed):
     P.assert16(got, ref, f"dense non-partition L={L} D={D}")
 
 
+def test_fwd_dense_mask_many_rows():
+    """More batch rows than one wavefront's lanes (the gated launches read
+    the per-row flags 64 at a time): even rows chain partitions, odd rows
+    random masks."""
+    print("[fwd dense many rows] B=70 L=40 D=16", flush=True)
+    m = _mpattn()
+    B, L, D = 70, 40, 16
+    xs, cid, kp = P.fwd_inputs(B, 1, L, D, torch.bfloat16, seed=700, nchains=3)
+    c = torch.from_numpy(cid)
+    cm = c[:, :, None] != c[:, None, :]
+    g = torch.Generator().manual_seed(70)
+    rnd = torch.rand(B, L, L, generator=g) < 0.5
+    cm[1::2] = rnd[1::2]
+    out = m.fused_multi_pathway_attention(*[x.to(DEV) for x in xs], cm.to(DEV), training=False,
+                                          key_padding_mask=torch.from_numpy(kp).to(DEV), rope=True,
+                                          scale=D ** -0.5)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy().astype(np.float64)
+    a = [x.double().numpy() for x in xs]
+    ref, _ = orc.mpattn_forward(*a, chain_mask=cm.numpy(), key_pad=kp, rope=True, scale=D ** -0.5)
+    P.assert16(got, ref, "dense many rows")
+
+
 def test_fwd_prerotated_contract():
     """Reference contract: q pre-scaled, q/k pre-rotated, scale 1, dense mask."""
     print("[fwd prerotated dense]", flush=True)
