@@ -951,6 +951,19 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
     };
     // probability of slot value x of S (or S' when folded)
     auto prob = [&](float x) { return FOLDC ? fast_exp2(x) : fast_exp2(fmaf(x, c, l2)); };
+    f32x16 ndlv;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ndlv[i] = dl;
+    auto dp_of = [&](const v8* aop, const v8* bop) {
+        if constexpr (FOLDC) {
+            f32x16 acc = ndlv;
+#pragma unroll
+            for (int kk = 0; kk < BS::NKK; ++kk) acc = E::mma(aop[kk], bop[kk], acc);
+            return acc;
+        }
+        return mma_kloop(aop, bop);
+    };
+    const float dlx = FOLDC ? 0.f : dl;  // -Delta left for dscore (0 when folded)
 
     // One 32-key subtile of pathway PW; masked: the subtile mixes pathways
     // (or holds padded keys), so only its pairs on PW count.
@@ -963,13 +976,13 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
             va[kk] = rop(stage, 1, st, kk);
         }
         const f32x16 sv = s_of(ka, qf);
-        const f32x16 dp = mma_kloop(va, dof);
+        const f32x16 dp = dp_of(va, dof);
         float dsv[16];
         if (!masked) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const float pv = prob(sv[i]);
-                dsv[i] = dscore(pv, dpe(dp[i], k0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8)), dl);
+                dsv[i] = FOLDC ? pv * dp[i] : dscore(pv, dpe(dp[i], k0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8)), dlx);
             }
         } else {
 #pragma unroll
@@ -991,7 +1004,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
                     }
                     const bool on = ck != kPadChain && sm_ == (PW == 0);
                     const float pv = on ? prob(sv[i]) : 0.f;
-                    dsv[i] = dscore(pv, dpe(dp[i], k0 + kl + t), dl);
+                    dsv[i] = FOLDC ? pv * dp[i] : dscore(pv, dpe(dp[i], k0 + kl + t), dlx);
                 }
             }
         }
