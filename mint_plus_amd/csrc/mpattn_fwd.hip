@@ -416,7 +416,9 @@ void fwd_kernel(const FwdArgs args) {
     const mpattn_fwd_params& p = args.p;
 
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * S::STAGE];
-    __shared__ __attribute__((aligned(16))) int scid[W][NBUF][kBN];
+    // effective chain ids of each stage's keys (one copy per workgroup, by
+    // its last wavefront, which has the fewest tile copies)
+    __shared__ __attribute__((aligned(16))) int scid[NBUF][kBN];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -505,7 +507,8 @@ void fwd_kernel(const FwdArgs args) {
     }
     const char* const keff_c = reinterpret_cast<const char*>(keff_b);
     const unsigned smem_base = lds_addr(smem);
-    const unsigned scid_base = lds_addr(&scid[wave][0][0]);
+    const unsigned scid_base = lds_addr(&scid[0][0]);
+    const bool cidw = wave == W - 1;  // (uniform)
 
     // ---- copy stage s into buffer bf ----
     // Returns the number of vector-memory instructions issued (uniform).
@@ -522,7 +525,7 @@ void fwd_kernel(const FwdArgs args) {
             for (int j = 0; j < NJ; ++j)
                 if (TOT % W == 0 || dten[j] < 4)  // (idle copies of the last round)
                     dma16(dsb[j] + (int64_t)k0 * dstr[j], vo[j], lb + dlds[j]);
-            dma4(keff_c + k0 * 4, (unsigned)lane * 4, scid_base + bf * kBN * 4);
+            if (cidw) dma4(keff_c + k0 * 4, (unsigned)lane * 4, scid_base + bf * kBN * 4);
             m0_restore(m0v);
         };
         if (k0 + kBN <= L) {
@@ -541,7 +544,7 @@ void fwd_kernel(const FwdArgs args) {
             }
             copies(vo);
         }
-        int n = 1;
+        int n = cidw ? 1 : 0;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) n += (TOT % W == 0 || dten[j] < 4) ? 1 : 0;
         return n;
@@ -1246,7 +1249,7 @@ void fwd_kernel(const FwdArgs args) {
             done = fast_stage(IC<0>{}, stage, c0[0], c0[0], s * kBN);
         }
         if (done != (1 << QB) - 1) {
-            const int* cid = &scid[wave][bf][0];
+            const int* cid = &scid[bf][0];
             const int k0 = s * kBN;
             for_blocks<QB>([&](auto u_c) {
                 constexpr int u = decltype(u_c)::value;
