@@ -977,14 +977,17 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
         }
         const f32x16 sv = s_of(ka, qf);
         const f32x16 dp = dp_of(va, dof);
+        // dS of every pair, then (masked) the pairs off the pathway set to 0
+        // in place: a select, so an overflowed P off the pathway is dropped
+        // whole, and both kinds of subtile feed one dQ product (the
+        // accumulators keep their registers across the branch).
         float dsv[16];
-        if (!masked) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float pv = prob(sv[i]);
-                dsv[i] = FOLDC ? pv * dp[i] : dscore(pv, dpe(dp[i], k0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8)), dlx);
-            }
-        } else {
+        for (int i = 0; i < 16; ++i) {
+            const float pv = prob(sv[i]);
+            dsv[i] = FOLDC ? pv * dp[i] : dscore(pv, dpe(dp[i], k0 + st * 32 + 16 * (i / 8) + 8 * hh + (i % 8)), dlx);
+        }
+        if (masked) {
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 const int kl = st * 32 + 16 * cc + 8 * hh;
@@ -1003,8 +1006,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
                         sm_ = ck == cq;
                     }
                     const bool on = ck != kPadChain && sm_ == (PW == 0);
-                    const float pv = on ? prob(sv[i]) : 0.f;
-                    dsv[i] = FOLDC ? pv * dp[i] : dscore(pv, dpe(dp[i], k0 + kl + t), dlx);
+                    dsv[i] = on ? dsv[i] : 0.f;
                 }
             }
         }
@@ -1109,8 +1111,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
             const int i = 2 * s + st - sub0;
             const int md = kmode(__builtin_amdgcn_readlane(ksw.x, i), __builtin_amdgcn_readlane(ksw.y, i),
                                  __builtin_amdgcn_readlane(ksw.z, i));
-            if (md == PW) subtile(stage, cid, st, false, k0);
-            else if (md == 2) subtile(stage, cid, st, true, k0);
+            if (md == PW || md == 2) subtile(stage, cid, st, md == 2, k0);
         }
         if constexpr (DENSE) {
 #pragma unroll
