@@ -81,8 +81,15 @@ int check_common(int B, int H, int L, int D, int dtype, int rope, float scale,
             return fail(MPATTN_ERR_UNSUPPORTED, "rope tables not 16-byte aligned");
     }
     if (sqrt_softmax != 0 && sqrt_softmax != 1) return fail(MPATTN_ERR_INVALID, "sqrt_softmax must be 0/1");
-    const int64_t nblk = (int64_t)B * H * ((L + 127) / 128);
-    if (nblk > 0x7fffffffLL || (int64_t)L * 4 > 0x7fffffffLL)
+    // Every launch stays below 2^32 work-items (HIP's limit per grid): at
+    // most 24 per padded row (the backward's prep: up to 8 for Delta and 12
+    // for the RoPE rotations), and with a dense mask 1/16 per mask element
+    // plus 64 per batch row and query (its label and block checks).
+    // (in double: the products of extreme arguments overflow int64)
+    const double lim = 4294967295.0, Lp = (double)(((int64_t)L + 127) / 128 * 128);
+    const double rows = (double)B * H * Lp;
+    const bool mask_big = chain_mask && (double)B * Lp * (Lp / 16) + (double)B * Lp * 64 > lim;
+    if (rows * 24 > lim || mask_big || (int64_t)L * 4 > 0x7fffffffLL)
         return fail(MPATTN_ERR_UNSUPPORTED, "problem too large for one launch");
     return MPATTN_OK;
 }

@@ -16,13 +16,14 @@
 // This is the exact gradient; the reference's Triton backward
 // (mint_plus/models/kernels/multi_pathway_attention_bwd.py:123-271) takes the
 // softmax row sum per key tile and applies the scale twice, and is not
-// followed. No atomics: dK/dV and dQ come from separate kernels, so results
-// are bitwise reproducible.
+// followed. No atomics: dK/dV and dQ come from separate workgroups, so
+// results are bitwise reproducible.
 //
 // Launches:
 //  1. bwd_prep_kernel: chain staging for keys (as the forward) and queries,
 //     Delta and LSE*log2(e) per query, RoPE-rotated Q_self/K_self.
-//  2. bwd_dkdv_kernel (key-stationary, one pathway per workgroup: a pair
+//  2. bwd_kernel: dK/dV workgroups, then dQ workgroups, in one grid.
+//     dK/dV (key-stationary, one pathway per workgroup: a pair
 //     contributes to one pathway only, so a workgroup holds that pathway's
 //     operands and accumulators): each wavefront keeps K and V of 32 keys in
 //     registers (MFMA B operands) and streams 64-query stages of Q (of the
@@ -30,8 +31,8 @@
 //     slot = query (query rows read bit-2/3-swapped), which is directly the A
 //     operand of dV += P^T dO and dK += dS^T Q; dO^T and Q^T are transpose
 //     reads of the row-major tiles.
-//  3. bwd_dq_kernel (query-stationary): the forward's structure plus
-//     dP^T = V dO^T and dQ^T += K^T dS^T.
+//     dQ (query-stationary): the forward's structure plus dP^T = V dO^T
+//     and dQ^T += K^T dS^T.
 #include <type_traits>
 
 #include "mpattn_bwd.h"
@@ -732,24 +733,6 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, uint64_t
                             p.rope_cos, p.rope_sin, key_live);
 }
 
-// Workgroup -> (key block, pathway, b*H + h): the two pathways of a key
-// block are neighbours in dispatch order (their K / V and Q tiles share the
-// XCD's L2).
-template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP>
-__global__ __launch_bounds__(W * 64) void bwd_dkdv_kernel(const BwdArgs a) {
-    using SL = DkdvStage<D, W, DENSE>;
-    __shared__ __attribute__((aligned(1024))) char smem[SL::SMEM];
-    __shared__ uint64_t wmask[W];
-    const int nkb = (a.p.L + 32 * W - 1) / (32 * W);
-    int blk, bh;
-    dispatch_order(2 * nkb, a.p.H, nullptr, 0, 0, 1, false, (int64_t)3 * a.p.L * D * sizeof(T), 2 << 20, blk, bh);
-    if (a.gate && ((a.gate_want == 0 && a.gate[a.p.B] == 0) ||  // (every row a partition)
-                   (a.gate[bh / a.p.H] != 0) != (a.gate_want != 0)))
-        return;  // (uniform)
-    if (blk & 1) dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, wmask, blk >> 1, bh);
-    else dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, wmask, blk >> 1, bh);
-}
-
 // ---------------------------------------------------------------------------
 // dQ: query-stationary.
 // ---------------------------------------------------------------------------
@@ -1131,22 +1114,41 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
                            p.rope_cos, p.rope_sin);
 }
 
-// Workgroup -> (query block, pathway, b*H + h), the two pathways of a
-// query block neighbours in dispatch order.
+// dK/dV and dQ in one grid (they read the same prep outputs and write
+// disjoint gradients): workgroups [0, nkv) run dK/dV, one per (key block,
+// pathway, b*H + h), the rest dQ, one per (query block, pathway, b*H + h);
+// the two pathways of a block are neighbours in dispatch order (their
+// tiles share the XCD's L2). dQ workgroups fill the last round of dK/dV's
+// instead of waiting for a grid boundary. One LDS allocation serves
+// whichever body the workgroup runs.
 template <typename T, int D, int W, bool ROPE, bool DENSE, bool SQRT, bool DROP>
-__global__ __launch_bounds__(W * 64) void bwd_dq_kernel(const BwdArgs a) {
-    using SL = DqStage<D, W>;
-    __shared__ __attribute__((aligned(1024))) char smem[SL::SMEM];
-    __shared__ __attribute__((aligned(16))) int scid[W][SL::NBUF][kBS];
+__global__ __launch_bounds__(W * 64) void bwd_kernel(const BwdArgs a, int nkv) {
+    using SK = DkdvStage<D, W, DENSE>;
+    using SQ = DqStage<D, W>;
+    constexpr int SMEM = SK::SMEM > SQ::SMEM ? SK::SMEM : SQ::SMEM;
+    __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+    __shared__ __attribute__((aligned(16))) int scid[W][SQ::NBUF][kBS];
     __shared__ uint64_t wmask[W];
-    const int nqb = (a.p.L + 32 * W - 1) / (32 * W);
+    const int nb = (a.p.L + 32 * W - 1) / (32 * W);
+    const int bid = blockIdx.x;
+    const bool kv = bid < nkv;
     int blk, bh;
-    dispatch_order(2 * nqb, a.p.H, nullptr, 0, 0, 1, false, (int64_t)2 * a.p.L * D * sizeof(T), 4 << 20, blk, bh);
+    if (kv)
+        dispatch_order_at(bid, nkv, 2 * nb, a.p.H, nullptr, 0, 0, 1, false, (int64_t)3 * a.p.L * D * sizeof(T),
+                          2 << 20, blk, bh);
+    else
+        dispatch_order_at(bid - nkv, (int)gridDim.x - nkv, 2 * nb, a.p.H, nullptr, 0, 0, 1, false,
+                          (int64_t)2 * a.p.L * D * sizeof(T), 4 << 20, blk, bh);
     if (a.gate && ((a.gate_want == 0 && a.gate[a.p.B] == 0) ||  // (every row a partition)
                    (a.gate[bh / a.p.H] != 0) != (a.gate_want != 0)))
         return;  // (uniform)
-    if (blk & 1) dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, scid, wmask, blk >> 1, bh);
-    else dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, scid, wmask, blk >> 1, bh);
+    if (kv) {
+        if (blk & 1) dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, wmask, blk >> 1, bh);
+        else dkdv_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, wmask, blk >> 1, bh);
+    } else {
+        if (blk & 1) dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 1>(a, smem, scid, wmask, blk >> 1, bh);
+        else dq_body<T, D, W, ROPE, DENSE, SQRT, DROP, 0>(a, smem, scid, wmask, blk >> 1, bh);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1225,17 +1227,13 @@ static hipError_t launch_bwd_t(const mpattn_bwd_params& p, hipStream_t stream) {
         ac.p.chain_id = a.label;
         ac.p.chain_mask = nullptr;
         ac.gate_want = 1;
-        hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, false, SQRT, DROP>), dim3(2 * grid), dim3(W * 64), 0,
-                           stream, ac);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, false, SQRT, DROP>), dim3(2 * grid), dim3(W * 64), 0, stream,
-                           ac);
+        hipLaunchKernelGGL((bwd_kernel<T, D, W, ROPE, false, SQRT, DROP>), dim3(4 * grid), dim3(W * 64), 0, stream,
+                           ac, (int)(2 * grid));
         if ((e = hipGetLastError()) != hipSuccess) return e;
         a.gate_want = 0;
     }
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(2 * grid), dim3(W * 64), 0, stream, a);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_dq_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(2 * grid), dim3(W * 64), 0, stream, a);
+    hipLaunchKernelGGL((bwd_kernel<T, D, W, ROPE, DENSE, SQRT, DROP>), dim3(4 * grid), dim3(W * 64), 0, stream, a,
+                       (int)(2 * grid));
     return hipGetLastError();
     }
 }

@@ -16,20 +16,21 @@
 //   With dropout (keep mask Z, r = 1 / (1 - p)): dV takes r Z w and dP_ij
 //   becomes r Z_ij dO_i . V_sel,j (the forward's definition in mpattn.h).
 //
-// Both kernels split the work by pathway: a workgroup computes the gradients
+// One launch, bwd32_kernel, runs dK/dV workgroups and then dQ workgroups.
+// Both split the work by pathway: a workgroup computes the gradients
 // of one pathway only, so it needs one pathway's operands and accumulators
 // (half the registers; a (query, key) pair contributes to exactly one
 // pathway). Workgroups of the two pathways of one row block are adjacent in
 // dispatch order, so they share their XCD's L2.
 //
-//  * bwd32_dkdv_kernel (key-stationary): 4 wavefronts x 32 keys. K and V of
+//  * dK/dV (key-stationary): 4 wavefronts x 32 keys. K and V of
 //    the wave's keys sit in registers as MFMA B operands (lane l: dims
 //    2*kk + l/32 of key l%32). 32-query subtiles of Q, dO, LSE2, Delta and
 //    chain ids stream through LDS, double-buffered. S = Q K^T and dP = dO V^T
 //    read query rows in the order pi(r) = 2*(4*(r/8) + r%4) + (r/4)%2, so
 //    slot i of lane half hh holds query 2*i + hh: the B operand of step i of
 //    dV^T += dO^T P and dK^T += Q^T dS.
-//  * bwd32_dq_kernel (query-stationary): the fp32 forward's structure
+//  * dQ (query-stationary): the fp32 forward's structure
 //    (S^T = K Q^T with Q in registers), plus dP^T = V dO^T and
 //    dQ^T += K^T dS^T.
 // Subtiles are classified from the prep kernel's chain summaries: all pairs on
@@ -297,19 +298,6 @@ __device__ void dkdv32_body(const BwdArgs& a, float* smem, int* sint, int kb, in
     }
 }
 
-template <int D, bool ROPE, bool DENSE, bool SQRT, bool DROP>
-__global__ __launch_bounds__(256) void bwd32_dkdv_kernel(const BwdArgs a) {
-    __shared__ float smem[Shape32<D>::SMEM];
-    __shared__ int sint[2 * 3 * kTB];
-    const int nkb = (a.p.L + 127) / 128;
-    const int g = xcd_remap(blockIdx.x, gridDim.x);
-    const int pw = g & 1, rest = g >> 1;
-    const int kb = rest % nkb, bh = rest / nkb;
-    const int b = bh / a.p.H, h = bh % a.p.H;
-    if (pw == 0) dkdv32_body<D, ROPE, DENSE, SQRT, DROP, 0>(a, smem, sint, kb, b, h);
-    else dkdv32_body<D, ROPE, DENSE, SQRT, DROP, 1>(a, smem, sint, kb, b, h);
-}
-
 // ---------------------------------------------------------------------------
 // dQ of pathway PW for 128 queries.
 // ---------------------------------------------------------------------------
@@ -435,27 +423,36 @@ __device__ void dq32_body(const BwdArgs& a, float* smem, int* sint, int qb, int 
                         ROPE && PW == 0, p.rope_cos, p.rope_sin, 0xffffffffu);
 }
 
+// dK/dV and dQ in one grid (same inputs, disjoint outputs): workgroups
+// [0, nkv) compute dK/dV, one per (key block, pathway, b*H + h), the rest
+// dQ, one per (query block, pathway, b*H + h). At the 8M shape each half
+// has fewer workgroups than the GPU has CUs, so the two run side by side.
 template <int D, bool ROPE, bool DENSE, bool SQRT, bool DROP>
-__global__ __launch_bounds__(256) void bwd32_dq_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(256) void bwd32_kernel(const BwdArgs a, int nkv) {
     __shared__ float smem[Shape32<D>::SMEM];
-    __shared__ int sint[2 * kTB];
-    const int nqb = (a.p.L + 127) / 128;
-    const int g = xcd_remap(blockIdx.x, gridDim.x);
+    __shared__ int sint[2 * 3 * kTB];
+    const int nb = (a.p.L + 127) / 128;
+    const int bid = blockIdx.x;
+    const bool kv = bid < nkv;
+    const int g = kv ? xcd_remap(bid, nkv) : xcd_remap(bid - nkv, (int)gridDim.x - nkv);
     const int pw = g & 1, rest = g >> 1;
-    const int qb = rest % nqb, bh = rest / nqb;
+    const int rb = rest % nb, bh = rest / nb;
     const int b = bh / a.p.H, h = bh % a.p.H;
-    if (pw == 0) dq32_body<D, ROPE, DENSE, SQRT, DROP, 0>(a, smem, sint, qb, b, h);
-    else dq32_body<D, ROPE, DENSE, SQRT, DROP, 1>(a, smem, sint, qb, b, h);
+    if (kv) {
+        if (pw == 0) dkdv32_body<D, ROPE, DENSE, SQRT, DROP, 0>(a, smem, sint, rb, b, h);
+        else dkdv32_body<D, ROPE, DENSE, SQRT, DROP, 1>(a, smem, sint, rb, b, h);
+    } else {
+        if (pw == 0) dq32_body<D, ROPE, DENSE, SQRT, DROP, 0>(a, smem, sint, rb, b, h);
+        else dq32_body<D, ROPE, DENSE, SQRT, DROP, 1>(a, smem, sint, rb, b, h);
+    }
 }
 
 template <int D, bool ROPE, bool DENSE, bool SQRT, bool DROP>
 hipError_t launch32(const BwdArgs& a, hipStream_t stream) {
     const int nb = (a.p.L + 127) / 128;
     const unsigned grid = (unsigned)(2 * (int64_t)a.p.B * a.p.H * nb);
-    hipLaunchKernelGGL((bwd32_dkdv_kernel<D, ROPE, DENSE, SQRT, DROP>), dim3(grid), dim3(256), 0, stream, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd32_dq_kernel<D, ROPE, DENSE, SQRT, DROP>), dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((bwd32_kernel<D, ROPE, DENSE, SQRT, DROP>), dim3(2 * grid), dim3(256), 0, stream, a,
+                       (int)grid);
     return hipGetLastError();
 }
 

@@ -146,11 +146,14 @@ __device__ inline void order_in_share(int xcd, int slot, int nblk_bh, int ngrp, 
 // Workgroup -> (row block, b*H + h) for a grid of one workgroup per block:
 // order_in_share over the XCD shares when the grid splits evenly over the 8
 // XCDs (dispatch is round-robin over them), else xcd_remap's order.
-__device__ inline void dispatch_order(int nblk_bh, int H, const int4* sums, int64_t sums_per_b, int nsum,
-                                      int rows32, bool pad_heavy, int64_t group_bytes, int64_t budget,
-                                      int& blk, int& bh) {
+// `bid` / `nblk`: the workgroup's index among the `nblk` workgroups of this
+// mapping (a grid may host several mappings back to back; the XCD of `bid`
+// is then the hardware's one when the mappings before it hold a multiple of
+// 8 workgroups, and the mapping is a bijection either way).
+__device__ inline void dispatch_order_at(int bid, int nblk, int nblk_bh, int H, const int4* sums,
+                                         int64_t sums_per_b, int nsum, int rows32, bool pad_heavy,
+                                         int64_t group_bytes, int64_t budget, int& blk, int& bh) {
     constexpr int kXcd = 8;
-    const int nblk = gridDim.x, bid = blockIdx.x;
     const int per = nblk / kXcd;
     if (nblk % kXcd == 0 && per % nblk_bh == 0) {
         order_in_share(bid % kXcd, bid / kXcd, nblk_bh, per / nblk_bh, H, sums, sums_per_b, nsum, rows32,
@@ -160,6 +163,13 @@ __device__ inline void dispatch_order(int nblk_bh, int H, const int4* sums, int6
         blk = __builtin_amdgcn_readfirstlane(g % nblk_bh);
         bh = __builtin_amdgcn_readfirstlane(g / nblk_bh);
     }
+}
+
+__device__ inline void dispatch_order(int nblk_bh, int H, const int4* sums, int64_t sums_per_b, int nsum,
+                                      int rows32, bool pad_heavy, int64_t group_bytes, int64_t budget,
+                                      int& blk, int& bh) {
+    dispatch_order_at(blockIdx.x, gridDim.x, nblk_bh, H, sums, sums_per_b, nsum, rows32, pad_heavy, group_bytes,
+                      budget, blk, bh);
 }
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -142,6 +142,10 @@ FWD_CASES = [
     (dict(v_multi=_lib.Tensor4(1 << 20, 40960, 2048, 36)), _lib.MPATTN_ERR_UNSUPPORTED, "multiples"),
     (dict(workspace_bytes=16), _lib.MPATTN_ERR_INVALID, "workspace"),
     (dict(workspace=(1 << 24) + 16), _lib.MPATTN_ERR_INVALID, "workspace"),
+    # grids past 2^32 work-items: 24 per padded row, and a dense mask's checks
+    (dict(B=1 << 16, H=64, L=1024), _lib.MPATTN_ERR_UNSUPPORTED, "too large for one launch"),
+    (dict(chain_id=None, chain_mask=1 << 23, B=64, H=1, L=1 << 16), _lib.MPATTN_ERR_UNSUPPORTED,
+     "too large for one launch"),
 ]
 
 
@@ -212,6 +216,19 @@ def test_bwd_rejects_rows_past_32bit_offsets(lib, name):
     assert lib.mpattn_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_UNSUPPORTED
     assert "32-bit row offsets" in lib.mpattn_last_error().decode()
     assert name in lib.mpattn_last_error().decode()
+
+
+def test_bwd_rejects_grid_past_32bit_work_items(lib):
+    """dK/dV and dQ run as one grid of 4 B H ceil(L/128) workgroups and the
+    prep at up to 20 threads per row: shapes whose launches would pass 2^32
+    work-items are refused before anything is enqueued."""
+    p = _bwd_params(B=1 << 16, H=64, L=1024)
+    assert lib.mpattn_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_UNSUPPORTED
+    assert "too large for one launch" in lib.mpattn_last_error().decode()
+    # 4096 * 44 rows of 1024: 24 work-items per row pass 2^32
+    p = _bwd_params(B=1 << 12, H=44, L=1024)
+    assert lib.mpattn_bwd(ctypes.byref(p), None) == _lib.MPATTN_ERR_UNSUPPORTED
+    assert "too large for one launch" in lib.mpattn_last_error().decode()
 
 
 def test_bwd_rejects_dense_mask_past_32bit_offsets(lib):
