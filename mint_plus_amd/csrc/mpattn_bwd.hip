@@ -377,6 +377,10 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a, char* smem, uint64_t
     const bool kvalid = ckey != kPadChain;
     const int kc_min = __builtin_amdgcn_readfirstlane(wave_min_i(kvalid ? ckey : INT32_MAX));
     const int kc_max = __builtin_amdgcn_readfirstlane(wave_max_i(kvalid ? ckey : INT32_MIN));
+    // Keys on several chains: no query stage is skipped and every pass is
+    // masked, and the workgroup's stage barriers wait for this wavefront,
+    // so it issues ahead of the wavefronts it shares a SIMD with.
+    if (kc_min < kc_max) __builtin_amdgcn_s_setprio(3);
     // Padded keys are not masked in the loop: a lane's probabilities enter only
     // its own key's rows of dV and dK, which the epilogue writes as zeros.
     const uint32_t key_live = (uint32_t)__builtin_amdgcn_ballot_w64(kvalid);
@@ -812,6 +816,9 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int (*scid
         cq = qin ? p.chain_id[(int64_t)b * L + q] : 0;
         cq_min = __builtin_amdgcn_readfirstlane(wave_min_i(qin ? cq : INT32_MAX));
         cq_max = __builtin_amdgcn_readfirstlane(wave_max_i(qin ? cq : INT32_MIN));
+        // Queries on several chains: every subtile is masked and the stage
+        // barriers wait for this wavefront (as in dK/dV).
+        if (cq_min < cq_max) __builtin_amdgcn_s_setprio(3);
     } else {
         mrow = p.chain_mask + (int64_t)b * p.mask_stride_b + (int64_t)(qin ? q : 0) * p.mask_stride_q;
     }

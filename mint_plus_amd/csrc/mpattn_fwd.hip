@@ -647,6 +647,13 @@ void fwd_kernel(const FwdArgs args) {
             cq_min[u] = __builtin_amdgcn_readfirstlane(cq_min[u]);
             cq_max[u] = __builtin_amdgcn_readfirstlane(cq_max[u]);
         }
+        // A wavefront whose queries span chains runs its subtiles on both
+        // pathways, and its workgroup's stage barriers wait for it: it issues
+        // ahead of the wavefronts it shares a SIMD with.
+        bool qstraddle = false;
+#pragma unroll
+        for (int u = 0; u < QB; ++u) qstraddle = qstraddle || cq_min[u] != cq_max[u];
+        if (qstraddle) __builtin_amdgcn_s_setprio(3);
     }
     const uint8_t* mrow[QB];
 #pragma unroll
