@@ -578,8 +578,10 @@ def bench_combine(args, dev, b=8):
     150M shape with B=8: two (B, H, L, L) bf16 logit tensors, the (B, L, L)
     bool mask and two value tensors. Algorithmic bytes: fwd reads 2 logits +
     mask + 2 values and writes O; bwd reads the same plus dO and writes both
-    d_logits and both d_values (the kernels read the logits three times: the
-    statistics pass, the d_logits pass and the dV pass)."""
+    d_logits and both d_values. ``bwd`` is the reference's signature (no
+    forward statistics: a statistics pass reads both logit tensors first);
+    ``bwd_fwdstats`` is the autograd path, given the forward's LSE and O
+    (Delta = dO . O from them, no statistics pass); its bytes add O and LSE."""
     from mint_plus_amd import _lib
     g = torch.Generator(device=dev).manual_seed(77)
     il = (torch.randn(b, H, L, L, device=dev, generator=g) * 2).to(torch.bfloat16)
@@ -600,9 +602,12 @@ def bench_combine(args, dev, b=8):
            "data": "synthetic logits N(0,4), 2 chains",
            "config": {"workload": "fused_multimer_combine fwd / bwd", "B": b, "H": H, "L": L,
                       "D": D}}
+    out, lse = _lib.mpattn_combine_fwd(il, el, cm, vs, vm, need_lse=True)
     for name, fn, nbytes in (
             ("fwd", lambda: _lib.mpattn_combine_fwd(il, el, cm, vs, vm), fwd_bytes),
-            ("bwd", lambda: _lib.mpattn_combine_bwd(il, el, cm, vs, vm, go), bwd_bytes)):
+            ("bwd", lambda: _lib.mpattn_combine_bwd(il, el, cm, vs, vm, go), bwd_bytes),
+            ("bwd_fwdstats", lambda: _lib.mpattn_combine_bwd(il, el, cm, vs, vm, go, lse=lse, out=out),
+             bwd_bytes + vb + b * H * L * 4)):
         _, per = timed(fn, max(10, args.steps // 4), args.warmup, stream)
         med = statistics.median(per)
         res[f"{name}_ms"] = round(med, 4)

@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define MPATTN_VERSION 5
+#define MPATTN_VERSION 6
 
 enum {
     MPATTN_OK = 0,
@@ -199,6 +199,13 @@ typedef struct mpattn_combine_bwd_params {
     int32_t dtype;
     float dropout_p;         /* the forward's dropout_p and dropout_seed    */
     uint64_t dropout_seed;
+    /* Optional (no counterpart in the reference, whose backward recomputes
+     * the row statistics): the forward's (B,H,L) fp32 log-sum-exp (from
+     * mpattn_combine_fwd's lse) and its output O. With lse non-NULL the
+     * backward takes LSE from it and Delta = dO . O from out, instead of a
+     * statistics pass over both logit tensors; NULL: that pass runs. */
+    const float *lse;
+    mpattn_tensor out;       /* (B, H, L, D), read when lse is non-NULL     */
 } mpattn_combine_bwd_params;
 
 /* Forward of the combine: O = softmax(where(mask, inter, intra)) split by

@@ -115,6 +115,7 @@ class CombineBwdParams(ctypes.Structure):
         ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("L", ctypes.c_int32), ("D", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
         ("dropout_p", ctypes.c_float), ("dropout_seed", ctypes.c_uint64),
+        ("lse", ctypes.c_void_p), ("out", Tensor4),
     ]
 
 
@@ -463,9 +464,13 @@ def mpattn_combine_fwd(intra_logits, inter_logits, chain_mask, intra_values, int
 
 
 def mpattn_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values, inter_values,
-                       grad_out, *, dropout_p=0.0, dropout_seed=0):
+                       grad_out, *, dropout_p=0.0, dropout_seed=0, lse=None, out=None):
     """Launch the combine backward; returns (d_intra_logits, d_inter_logits,
-    d_intra_values, d_inter_values) in the inputs' dtype."""
+    d_intra_values, d_inter_values) in the inputs' dtype.
+
+    ``lse`` / ``out``: the forward's fp32 (B, H, L) log-sum-exp and output
+    (``mpattn_combine_fwd(..., need_lse=True)``); given both, the row
+    statistics come from them instead of a pass over both logit tensors."""
     B, H, L, D, cm = _combine_common(intra_logits, inter_logits, chain_mask, intra_values,
                                      inter_values)
     _common_checks([intra_values, grad_out], ["intra_values", "grad_out"])
@@ -495,8 +500,21 @@ def mpattn_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values, int
     p.dtype = _DTYPES[vs.dtype]
     p.dropout_p = float(dropout_p)
     p.dropout_seed = int(dropout_seed) & 0xFFFFFFFFFFFFFFFF
+    if (lse is None) != (out is None):
+        raise ValueError("mpattn_combine_bwd: give both lse and out, or neither")
+    fo = None
+    if lse is not None:
+        if lse.dtype != torch.float32 or tuple(lse.shape) != (B, H, L) or not lse.is_contiguous():
+            raise ValueError("mpattn_combine_bwd: lse must be a contiguous fp32 (B, H, L) tensor")
+        if tuple(out.shape) != (B, H, L, D) or out.dtype != vs.dtype or out.device != dev:
+            raise ValueError("mpattn_combine_bwd: out must be the forward's (B, H, L, D) output")
+        if lse.device != dev:
+            raise ValueError("mpattn_combine_bwd: lse is on another device")
+        fo = _aligned(out)
+        p.lse, p.out = lse.data_ptr(), _t4(fo)
     rc = lib.mpattn_combine_bwd(ctypes.byref(p), _stream_handle(dev))
     _check(rc, "mpattn_combine_bwd")
+    del fo
     del il, el, vs, vm, go, cm, ws
     return d_il, d_el, d_vs, d_vm
 

@@ -115,8 +115,10 @@ int check_combine(int B, int H, int L, int D, int dtype, const uint8_t* mask, in
     if (msb < 0 || msq < 0 || msk < 0) return fail(MPATTN_ERR_UNSUPPORTED, "chain_mask: negative stride");
     if (!(dropout_p >= 0.f && dropout_p < 1.f))
         return fail(MPATTN_ERR_INVALID, "dropout_p must be in [0, 1) (got %g)", (double)dropout_p);
-    const int64_t nblk = (int64_t)B * H * ((L + 63) / 64);
-    if (nblk > 0x7fffffffLL) return fail(MPATTN_ERR_UNSUPPORTED, "problem too large for one launch");
+    // every launch below 2^32 work-items: at most 8 per row (the backward's
+    // Delta from the forward's output; the others take 2 to 4)
+    if ((double)B * H * (((int64_t)L + 127) / 128 * 128) * 8 > 4294967295.0)
+        return fail(MPATTN_ERR_UNSUPPORTED, "problem too large for one launch");
     return MPATTN_OK;
 }
 
@@ -282,6 +284,10 @@ int mpattn_combine_bwd(const mpattn_combine_bwd_params* p, void* stream) {
     for (int i = 0; i < 4; ++i)
         if (!lt[i]->ptr || lt[i]->stride_b < 0 || lt[i]->stride_h < 0 || lt[i]->stride_t < 0)
             return fail(MPATTN_ERR_INVALID, "%s: null pointer or negative stride", ln[i]);
+    if (p->lse) {  // the forward's statistics: LSE and its output O
+        if ((uintptr_t)p->lse % 4) return fail(MPATTN_ERR_INVALID, "lse misaligned");
+        if ((rc = check_tensor(p->out, "out", es, false))) return rc;
+    }
     {
         const int64_t need = mpattn::combine_bwd_workspace_bytes(p->B, p->H, p->L);
         if (!p->workspace || (uintptr_t)p->workspace % 256 || p->workspace_bytes < need)

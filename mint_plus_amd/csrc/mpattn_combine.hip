@@ -960,10 +960,48 @@ void launch_dma(const CombineArgs& a, hipStream_t st) {
     }
 }
 
+// Delta = dO . O per row from the forward's output, for a backward given
+// the forward's LSE (no statistics pass): 8 lanes per row, 8 dims each.
+template <typename T>
+__global__ __launch_bounds__(256) void combine_delta_kernel(const CombineArgs a) {
+    const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t row = item >> 3;  // (b * H + h) * L + q
+    const int c = (int)(item & 7);
+    const int64_t nrow = (int64_t)a.B * a.H * a.L;
+    float dot = 0.f;
+    if (row < nrow && c * 8 < a.D) {
+        const int q = (int)(row % a.L);
+        const int bh = (int)(row / a.L);
+        const int b = bh / a.H, h = bh % a.H;
+        const T* o = (const T*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)q * a.o_st;
+        const T* g = (const T*)a.go + b * a.g_sb + h * a.g_sh + (int64_t)q * a.g_st;
+#pragma unroll
+        for (int k = 0; k < 8; k += 4) {
+            float x[4], y[4];
+            load4f<T>(o, c * 8 + k, x);
+            load4f<T>(g, c * 8 + k, y);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dot += x[r] * y[r];
+        }
+    }
+    dot += __shfl_xor(dot, 4);
+    dot += __shfl_xor(dot, 2);
+    dot += __shfl_xor(dot, 1);
+    if (row < nrow && c == 0) a.delta[row] = dot;
+}
+
+// mode 0: forward; 1: backward with its statistics pass; 2: backward given
+// the forward's LSE and O (Delta from them, no pass over the logits).
 template <typename T, int ND, bool VEC>
 hipError_t launch_combine_t(const CombineArgs& a, int mode, hipStream_t st) {
     const int nqb = (a.L + 127) / 128, nkb = (a.L + 63) / 64;
     const int bh = a.B * a.H;
+    if (mode == 2) {
+        const int64_t nrow = (int64_t)bh * a.L;
+        hipLaunchKernelGGL(combine_delta_kernel<T>, dim3((unsigned)((nrow * 8 + 255) / 256)), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((combine_bwd_kernel<T, ND, VEC>), dim3(bh * nkb), dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
     if constexpr (sizeof(T) == 2 && VEC) {
         if (dma_ok(a)) {
             if (mode == 0) {
@@ -1067,15 +1105,21 @@ hipError_t launch_combine_bwd(const mpattn_combine_bwd_params& p, hipStream_t st
     char* ws = (char*)p.workspace;
     a.lse = (float*)ws;
     a.delta = (float*)(ws + combine_ws_offset_delta(p.B, p.H, p.L));
+    int mode = 1;
+    if (p.lse) {  // the forward's statistics (read only)
+        a.lse = const_cast<float*>(p.lse);
+        a.out = (void*)p.out.ptr; a.o_sb = p.out.stride_b; a.o_sh = p.out.stride_h; a.o_st = p.out.stride_t;
+        mode = 2;
+    }
     const int es = p.dtype == MPATTN_FP32 ? 4 : 2;
     // the d_logits stores use the same vector path as the logit loads
     const bool vec = vec_ok(a, es) &&
                      aligned_rows(a.dil, a.dil_sb, a.dil_sh, a.dil_st, es) &&
                      aligned_rows(a.del, a.del_sb, a.del_sh, a.del_st, es);
     switch (p.dtype) {
-        case MPATTN_BF16: return launch_combine_d<bf16_t>(a, vec, 1, st);
-        case MPATTN_FP16: return launch_combine_d<fp16_t>(a, vec, 1, st);
-        default: return launch_combine_d<float>(a, vec, 1, st);
+        case MPATTN_BF16: return launch_combine_d<bf16_t>(a, vec, mode, st);
+        case MPATTN_FP16: return launch_combine_d<fp16_t>(a, vec, mode, st);
+        default: return launch_combine_d<float>(a, vec, mode, st);
     }
 }
 

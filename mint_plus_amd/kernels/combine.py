@@ -34,32 +34,40 @@ def fused_multimer_combine(intra_logits, inter_logits, chain_mask, intra_values,
 
 
 def fused_multimer_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values,
-                               inter_values, grad_output, dropout_p=0.0, *, dropout_seed=0):
+                               inter_values, grad_output, dropout_p=0.0, *, dropout_seed=0,
+                               lse=None, output=None):
     """(d_intra_logits, d_inter_logits, d_intra_values, d_inter_values) of the
     combine (kernels/__init__.py:247-286), in the inputs' dtype; with dropout,
-    ``dropout_seed`` must be the forward's."""
+    ``dropout_seed`` must be the forward's. ``lse`` / ``output``: the
+    forward's log-sum-exp and output (both or neither); given, the row
+    statistics come from them instead of a pass over both logit tensors."""
     _check_mask(chain_mask)
     return _lib.mpattn_combine_bwd(intra_logits, inter_logits, chain_mask, intra_values,
                                    inter_values, grad_output, dropout_p=dropout_p,
-                                   dropout_seed=dropout_seed)
+                                   dropout_seed=dropout_seed, lse=lse, out=output)
 
 
 class _MultimerCombineFn(Function):
     @staticmethod
     def forward(ctx, intra_logits, inter_logits, chain_mask, intra_values, inter_values,
                 dropout_p, dropout_seed):
-        ctx.save_for_backward(intra_logits, inter_logits, chain_mask, intra_values, inter_values)
+        # The forward's LSE and output go to the backward, which then needs
+        # no statistics pass over the two logit tensors.
+        out, lse = _lib.mpattn_combine_fwd(intra_logits, inter_logits, chain_mask, intra_values,
+                                           inter_values, dropout_p=dropout_p,
+                                           dropout_seed=dropout_seed, need_lse=True)
+        ctx.save_for_backward(intra_logits, inter_logits, chain_mask, intra_values, inter_values,
+                              out, lse)
         ctx.dropout_p, ctx.dropout_seed = dropout_p, dropout_seed
-        return fused_multimer_combine(intra_logits, inter_logits, chain_mask, intra_values,
-                                      inter_values, dropout_p=dropout_p, dropout_seed=dropout_seed)
+        return out
 
     @staticmethod
     def backward(ctx, grad_output):
-        il, el, cm, vs, vm = ctx.saved_tensors
+        il, el, cm, vs, vm, out, lse = ctx.saved_tensors
         with torch.no_grad():
             d_il, d_el, d_vs, d_vm = fused_multimer_combine_bwd(
                 il, el, cm, vs, vm, grad_output.contiguous(), dropout_p=ctx.dropout_p,
-                dropout_seed=ctx.dropout_seed)
+                dropout_seed=ctx.dropout_seed, lse=lse, output=out)
         return d_il, d_el, None, d_vs, d_vm, None, None
 
 

@@ -37,7 +37,7 @@ def test_exports_every_header_function(lib):
 
 
 def test_version_and_strings(lib):
-    assert lib.mpattn_version() == 5
+    assert lib.mpattn_version() == 6
     assert lib.mpattn_strerror(0) == b"success"
     assert lib.mpattn_strerror(-2) == b"unsupported configuration"
     assert lib.mpattn_strerror(-99) == b"unknown error"

@@ -88,6 +88,50 @@ def test_combine_bwd(dtype, D, L):
         check(a, r, dtype, f"{name} {dtype} D={D} L={L}", rel_fro=fro)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [16, 32, 64])
+@pytest.mark.parametrize("L", [64, 129, 208])
+@pytest.mark.parametrize("p", [0.0, 0.25])
+def test_combine_bwd_with_forward_stats(dtype, D, L, p):
+    """The backward given the forward's LSE and output (Delta = dO . O from
+    them, no statistics pass over the logits) against the oracle, and
+    against the backward that recomputes the statistics (LSE comes from the
+    same arithmetic; Delta differs by the rounding of the stored O)."""
+    print(f"[combine bwd fwd-stats] {dtype} D={D} L={L} p={p}", flush=True)
+    t, cm = make(2, 2, L, D, dtype, seed=300 + D + L)
+    g = [x.to(DEV) for x in t]
+    cmt = torch.from_numpy(cm).to(DEV)
+    m = _m()
+    out, lse = m._lib.mpattn_combine_fwd(g[0], g[1], cmt, g[2], g[3], dropout_p=p,
+                                         dropout_seed=11, need_lse=True)
+    fast = m.fused_multimer_combine_bwd(g[0], g[1], cmt, g[2], g[3], g[4], dropout_p=p,
+                                        dropout_seed=11, lse=lse, output=out)
+    slow = m.fused_multimer_combine_bwd(g[0], g[1], cmt, g[2], g[3], g[4], dropout_p=p,
+                                        dropout_seed=11)
+    torch.cuda.synchronize()
+    ref = orc.combine_backward(*[x.double().numpy() for x in t[:2]], cm,
+                               *[x.double().numpy() for x in t[2:]], dropout_p=p,
+                               dropout_seed=11)
+    fro = 1e-5 if dtype == torch.float32 else 2e-2
+    for name, a, b, r in zip(("d_intra_logits", "d_inter_logits", "d_vs", "d_vm"), fast, slow, ref):
+        assert a.dtype == dtype
+        check(a, r, dtype, f"{name} {dtype} D={D} L={L} p={p}", rel_fro=fro)
+        check(a, b.double().cpu().numpy(), dtype, f"{name} vs recomputed statistics")
+
+
+def test_combine_bwd_stats_arguments():
+    """lse without out (or out without lse) is refused before any launch."""
+    t, cm = make(1, 2, 64, 32, torch.bfloat16, seed=1)
+    g = [x.to(DEV) for x in t]
+    cmt = torch.from_numpy(cm).to(DEV)
+    lse = torch.zeros(1, 2, 64, dtype=torch.float32, device=DEV)
+    with pytest.raises(ValueError):
+        _m().fused_multimer_combine_bwd(g[0], g[1], cmt, g[2], g[3], g[4], lse=lse)
+    with pytest.raises(ValueError):
+        _m().fused_multimer_combine_bwd(g[0], g[1], cmt, g[2], g[3], g[4], lse=lse[:, :1],
+                                        output=g[2])
+
+
 def test_combine_all_padded_row_and_strided_logits():
     """A sample whose keys are all -inf gives zero output and gradients (the
     reference kernel would produce NaN); logits given as a strided slice of a
