@@ -750,6 +750,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ND == 1 ? 4
     rv8 ni, ne;
     uint64_t nm = 0;
     float nl = 0.f, nd = 0.f;
+    // The next step's dO chunk of this thread (16-bit: rows of 16-byte
+    // multiples; at most one chunk per thread): row q0 + gr, dims 8*gdc..
+    const int gr = tid / (DP / 8), gdc = tid % (DP / 8);
+    const bool gown = PF && tid < 32 * (DP / 8);
+    rv8 ngo{};
     auto fetch = [&](int q) {
         const int qc = min(q, L - 1);
         if (pfk) {
@@ -759,6 +764,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ND == 1 ? 4
         }
         nl = lse[qc];
         nd = dlt[qc];
+        if constexpr (PF) {
+            const int qr = q - tq + gr;  // (q is the step's first row + tq)
+            if (gown && qr < L && gdc < nch) ngo = *reinterpret_cast<const rv8*>(g + (int64_t)qr * a.g_st + gdc * 8);
+        }
     };
     fetch(tq);
     for (int q0 = 0; q0 < L; q0 += 32) {
@@ -786,7 +795,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ND == 1 ? 4
             }
             const float l = nl;
             dq = nd;
-            if (q0 + 32 < L) fetch(qq + 32);
+            if constexpr (!PF)
+                if (q0 + 32 < L) fetch(qq + 32);
             const bool ok = qq < L && l > -INFINITY;
             const float l2 = ok ? l * kLog2eC : 0.f;
             if (dropon) {
@@ -811,15 +821,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ND == 1 ? 4
                 }
             }
         }
-        // dO rows q0 .. q0+31 (rows >= L and dims >= D are zero).
+        // dO rows q0 .. q0+31 (rows >= L and dims >= D are zero); 16-bit:
+        // this thread's chunk was loaded with the previous step's fetch.
+        const rv8 cgo = ngo;
+        if constexpr (PF)
+            if (q0 + 32 < L) fetch(qq + 32);
         for (int c = tid; c < 32 * (DP / 8); c += 256) {
             const int r = c / (DP / 8), dc = c - r * (DP / 8);
             const int qr = q0 + r;
             float x[8];
             if (qr < L && dc < nch) {
-                const T* src = g + (int64_t)qr * a.g_st + dc * 8;
+                if constexpr (PF) {
 #pragma unroll
-                for (int j = 0; j < 8; j += 4) load4f<T>(src, j, x + j);
+                    for (int j = 0; j < 8; ++j) x[j] = (float)cgo[j];
+                } else {
+                    const T* src = g + (int64_t)qr * a.g_st + dc * 8;
+#pragma unroll
+                    for (int j = 0; j < 8; j += 4) load4f<T>(src, j, x + j);
+                }
             } else {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) x[j] = 0.f;
